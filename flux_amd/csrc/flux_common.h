@@ -1,0 +1,119 @@
+// Shared constants and device helpers for the gfx950 SmolLM2 token-loop kernels.
+//
+// Geometry is fixed by the reference (csrc/native_decode_runtime/
+// native_decode_runtime_cuda.cu:29-37, csrc/native_prefill_runtime/
+// native_prefill_runtime_cuda.cu:26-36); the vocabulary size and the cache
+// capacity are runtime values.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace flux {
+
+constexpr int kLayers = 30;
+constexpr int kHidden = 576;
+constexpr int kInter = 1536;
+constexpr int kQHeads = 9;
+constexpr int kKVHeads = 3;
+constexpr int kGroup = kQHeads / kKVHeads;  // query heads per KV head
+constexpr int kHeadDim = 64;
+constexpr int kQKV = (kQHeads + 2 * kKVHeads) * kHeadDim;  // 960
+constexpr int kGateUp = 2 * kInter;                        // 3072
+constexpr int kWave = 64;
+// The reference caps capacity at 8192 (native_decode_runtime_cuda.cu:36); the
+// benchmark configurations need 8320 and 8704 positions, so this build sizes
+// every kernel for 16384.
+constexpr int64_t kMaxCapacity = 16384;
+
+// Per-layer borrowed weights plus the layer's scalar parameters.
+struct LayerWeights {
+    const float* input_norm;  // [576]
+    const float* qkv;         // [960, 576]   packed cat(Wq, Wk, Wv)
+    const float* o_proj;      // [576, 576]
+    const float* post_norm;   // [576]
+    const float* gate_up;     // [3072, 576]  packed cat(Wgate, Wup)
+    const float* down;        // [576, 1536]
+    float eps;
+    float scale;  // attention scaling (head_dim^-0.5 for SmolLM2)
+};
+
+// ---------------------------------------------------------------------------
+// Wave64 helpers.  Butterfly (xor) reductions leave the identical value in every
+// lane because IEEE addition/max are commutative, so no broadcast is needed and
+// results are bitwise deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+template <int kWidth>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = kWidth / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Lane slicing of a 576-vector: lane owns [4l,4l+4) , [256+4l, 256+4l+4) and 512+l.
+__device__ __forceinline__ int slice576_index(int lane, int j) {
+    return j < 4 ? 4 * lane + j : (j < 8 ? 256 + 4 * lane + (j - 4) : 512 + lane);
+}
+
+// Lane slicing of a 1536-vector: six float4 chunks at 256*c + 4l.
+__device__ __forceinline__ int slice1536_index(int lane, int j) {
+    return 256 * (j >> 2) + 4 * lane + (j & 3);
+}
+
+__device__ __forceinline__ void load_row576(const float* __restrict__ row, int lane, float (&w)[9]) {
+    const float4 a = *reinterpret_cast<const float4*>(row + 4 * lane);
+    const float4 b = *reinterpret_cast<const float4*>(row + 256 + 4 * lane);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    w[8] = row[512 + lane];
+}
+
+__device__ __forceinline__ void load_row1536(const float* __restrict__ row, int lane, float (&w)[24]) {
+#pragma unroll
+    for (int c = 0; c < 6; ++c) {
+        const float4 a = *reinterpret_cast<const float4*>(row + 256 * c + 4 * lane);
+        w[4 * c + 0] = a.x; w[4 * c + 1] = a.y; w[4 * c + 2] = a.z; w[4 * c + 3] = a.w;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float dot_lane(const float (&x)[N], const float (&w)[N]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) acc = fmaf(x[j], w[j], acc);
+    return acc;
+}
+
+// HF RMSNorm rounding: weight * (h * (1 / sqrt(mean(h^2) + eps))) -- transformers
+// modeling_llama.py:53-68; reference kernel rmsnorm_cuda.cu:54-62.
+__device__ __forceinline__ float rms_inverse(float sum_squares, int width, float eps) {
+    const float mean = sum_squares / static_cast<float>(width);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// SiLU as torch's CPU kernel rounds it: x / (1 + exp(-x)).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Argmax ordering of greedy_generation_cuda.cu:20-37: NaN beats numbers, larger
+// value wins, ties go to the lower index.
+__device__ __forceinline__ bool argmax_precedes(float cv, int64_t ci, float iv, int64_t ii) {
+    const bool cn = cv != cv;
+    const bool in = iv != iv;
+    if (cn != in) return cn;
+    if (cn) return ci < ii;
+    return cv > iv || (cv == iv && ci < ii);
+}
+
+}  // namespace flux

@@ -1,0 +1,109 @@
+// Internal launcher interface between the C++ runtime and the gfx950 kernels.
+#pragma once
+
+#include "flux_common.h"
+
+#include <cstddef>
+#include <cstdint>
+
+namespace flux {
+
+// Upper bound on attention chunks per KV head in the fused kernel (grid <= 384).
+constexpr int kMaxAttnChunks = 128;
+
+struct DecodeArgs {
+    const LayerWeights* layers;  // device array [kLayers]
+    const float* embedding;      // [vocab, 576]
+    const float* lm_head;        // [vocab, 576]
+    const float* final_norm;     // [576]
+    float final_eps;
+    const float* rope_cos;       // [capacity, 64]
+    const float* rope_sin;
+    float* key_cache;            // [30, 3, capacity, 64]
+    float* value_cache;
+    float* logits;               // [vocab]
+    int64_t* input_token;
+    int64_t* generated;          // [generated_capacity]
+    int64_t* generation_step;
+    int64_t* position;
+    int64_t* cache_length;
+    uint64_t* ll;                // LL arena (ll_arena_words())
+    uint32_t* token_counter;
+    int32_t* error;
+    int64_t capacity;
+    int64_t vocab;
+    int64_t generated_capacity;
+    int steps;
+};
+
+// ---- fused decode ----
+size_t ll_arena_words();
+int fused_decode_threads();
+size_t fused_decode_dynamic_lds();
+int max_attention_positions(int grid);
+hipError_t fused_decode_occupancy(int* blocks_per_cu);
+hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream);
+
+// ---- isolated decode phases ----
+hipError_t launch_qkv_rope_cache(const float* hidden, const float* norm_w, float eps, const float* qkv_w,
+                                 const float* cos_table, const float* sin_table, const int64_t* position,
+                                 int64_t capacity, float* key_cache, float* value_cache, float* q_out, int grid,
+                                 hipStream_t stream);
+hipError_t launch_gqa_decode(const float* q, const float* key_cache, const float* value_cache, const int64_t* position,
+                             int64_t capacity, float scale, int chunks, float* partials, float* out,
+                             hipStream_t stream);
+int gqa_decode_max_positions(int chunks);
+hipError_t launch_linear576_residual(const float* x, const float* w, const float* residual, float* out, int rows,
+                                     int grid, hipStream_t stream);
+hipError_t launch_gate_up_swiglu(const float* hidden, const float* norm_w, float eps, const float* gate_up, float* out,
+                                 int grid, hipStream_t stream);
+hipError_t launch_down_residual(const float* s, const float* w, const float* residual, float* out, int grid,
+                                hipStream_t stream);
+hipError_t launch_lm_head_argmax(const float* hidden, const float* norm_w, float eps, const float* lm_head,
+                                 int64_t vocab, float* logits, float* part_v, int64_t* part_i, int grid,
+                                 int64_t* token, hipStream_t stream);
+hipError_t launch_argmax(const float* logits, int64_t n, int64_t* token, int64_t* generated, int64_t* step,
+                         int64_t generated_capacity, int64_t* position, const int64_t* attention_length,
+                         hipStream_t stream);
+hipError_t launch_install_state(const int64_t* token_src, int64_t position_value, int64_t step_value,
+                                bool write_generated0, int64_t* input_token, int64_t* position, int64_t* cache_length,
+                                int64_t* step, int64_t* generated, hipStream_t stream);
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows, int cols, float eps,
+                               hipStream_t stream);
+hipError_t launch_residual_rmsnorm_rows(const float* hidden, const float* residual, const float* w, float* norm_out,
+                                        float* residual_out, int64_t rows, int cols, float eps, hipStream_t stream);
+
+// ---- prefill ----
+enum class GemmEpilogue : int {
+    kStore = 0,         // C = A B^T
+    kResidual = 1,      // C = R + A B^T
+    kSwiglu = 2,        // gate/up interleaved tiles -> silu(g) * u into [M, N/2]
+    kQkvRope = 3,       // RoPE + head-major q + compact K/V cache rows
+};
+
+struct GemmArgs {
+    const float* a;     // [M, K] row-major
+    const float* b;     // [N, K] row-major (weights)
+    float* c;           // output (layout by epilogue)
+    const float* residual;
+    int64_t m;
+    int n;
+    int k;
+    // kQkvRope
+    const float* rope_cos;  // [capacity, 64] (row = position)
+    const float* rope_sin;
+    float* q_out;           // [9, M, 64]
+    float* key_cache;       // [3, capacity, 64]
+    float* value_cache;
+    int64_t capacity;
+};
+
+hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream);
+
+hipError_t launch_prefill_attention(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
+                                    int64_t capacity, float scale, float* out_rows, hipStream_t stream);
+
+hipError_t launch_embedding_gather(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
+                                   float* hidden, hipStream_t stream);
+
+}  // namespace flux

@@ -1,0 +1,361 @@
+// gfx950 prefill kernels: FP32-MFMA GEMMs with fused epilogues and a tiled
+// online-softmax causal GQA attention on FP32 MFMA.
+//
+// Reference path: csrc/native_prefill_runtime/native_prefill_runtime_cuda.cu:553-665
+// (cuBLAS SGEMM linear_fp32 :285-302, QKV RoPE/cache fill kernel :124-163, SwiGLU
+// csrc/packed_swiglu/packed_swiglu_cuda.cu:14-31, residual add :267-278, heads->rows
+// :249-265) and csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu:43-460
+// (online softmax with K/V tiles in shared memory, no score materialisation).
+//
+// MI355X design:
+//  * GEMM: 128x64 block tile, 4 waves stacked in M, each wave 32x64 computed with
+//    v_mfma_f32_32x32x2f32 (two 32x32 column tiles).  The epilogue consumes the
+//    accumulator layout directly: the two column tiles of a wave hold columns j
+//    and j+32 of the same rows, which is exactly the RoPE pair (QKV tile = one
+//    head) and the gate/up pair (gate/up tiles are interleaved 32+32).
+//  * Attention: one block per (64-query tile, query head); 4 waves x 16 queries.
+//    S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x4f32, so the S^T
+//    accumulators are already the B operand of the PV product (no transpose).
+
+#include "flux_common.h"
+#include "flux_kernels.h"
+
+#include <cfloat>
+#include <cmath>
+
+namespace flux {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+constexpr int kBK = 16;
+constexpr int kGemmThreads = 256;
+constexpr int kAPad = 4;
+
+// MFMA 32x32x2 accumulator element r of lane l -> (row, col) inside the 32x32 tile.
+__device__ __forceinline__ int mfma32_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+#pragma clang fp contract(off)
+__device__ __forceinline__ float rope_lo(float x, float paired, float c, float s) {
+    const float a = x * c;
+    const float b = (-paired) * s;
+    return a + b;
+}
+__device__ __forceinline__ float rope_hi(float x, float paired, float c, float s) {
+    const float a = x * c;
+    const float b = paired * s;
+    return a + b;
+}
+#pragma clang fp contract(fast)
+
+// Weight row used for virtual column `col` of the B operand.
+template <GemmEpilogue E>
+__device__ __forceinline__ int b_row(int col, int n) {
+    if constexpr (E == GemmEpilogue::kSwiglu) {
+        // Tile t (64 columns) = gate rows [32t, 32t+32) then up rows [half + 32t, ...).
+        const int half = n / 2;
+        const int t = col >> 6;
+        const int v = col & 63;
+        return v < 32 ? 32 * t + v : half + 32 * t + (v - 32);
+    } else {
+        return col;
+    }
+}
+
+template <GemmEpilogue E>
+__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
+    __shared__ float a_s[2][kBK][kBM + kAPad];
+    __shared__ float b_s[2][kBK][kBN + kAPad];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+    const int n0 = blockIdx.x * kBN;
+    const int K = args.k;
+
+    // Global -> LDS mapping: A tile 128x16 = 512 float4 (2 per thread), B 64x16 = 256 float4.
+    const int a_row = threadIdx.x >> 2;         // 0..63 (+64)
+    const int a_kq = (threadIdx.x & 3) * 4;     // 0,4,8,12
+    const int b_rowi = threadIdx.x >> 2;        // 0..63
+    const int64_t a_r0 = m0 + a_row;
+    const int64_t a_r1 = m0 + a_row + 64;
+    const float* a_p0 = args.a + (a_r0 < args.m ? a_r0 : 0) * K + a_kq;
+    const float* a_p1 = args.a + (a_r1 < args.m ? a_r1 : 0) * K + a_kq;
+    const bool a_ok0 = a_r0 < args.m;
+    const bool a_ok1 = a_r1 < args.m;
+    const float* b_p = args.b + static_cast<int64_t>(b_row<E>(n0 + b_rowi, args.n)) * K + a_kq;
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+
+    float4 ra0, ra1, rb;
+    auto load_stage = [&](int k0) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        ra0 = a_ok0 ? *reinterpret_cast<const float4*>(a_p0 + k0) : z;
+        ra1 = a_ok1 ? *reinterpret_cast<const float4*>(a_p1 + k0) : z;
+        rb = *reinterpret_cast<const float4*>(b_p + k0);
+    };
+    auto store_stage = [&](int buf) {
+        a_s[buf][a_kq + 0][a_row] = ra0.x; a_s[buf][a_kq + 1][a_row] = ra0.y;
+        a_s[buf][a_kq + 2][a_row] = ra0.z; a_s[buf][a_kq + 3][a_row] = ra0.w;
+        a_s[buf][a_kq + 0][a_row + 64] = ra1.x; a_s[buf][a_kq + 1][a_row + 64] = ra1.y;
+        a_s[buf][a_kq + 2][a_row + 64] = ra1.z; a_s[buf][a_kq + 3][a_row + 64] = ra1.w;
+        b_s[buf][a_kq + 0][b_rowi] = rb.x; b_s[buf][a_kq + 1][b_rowi] = rb.y;
+        b_s[buf][a_kq + 2][b_rowi] = rb.z; b_s[buf][a_kq + 3][b_rowi] = rb.w;
+    };
+
+    const int stages = K / kBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int s = 0; s < stages; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < stages) load_stage((s + 1) * kBK);
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 2) {
+            const float a = a_s[buf][kk + (lane >> 5)][wave * 32 + (lane & 31)];
+            const float b0 = b_s[buf][kk + (lane >> 5)][(lane & 31)];
+            const float b1 = b_s[buf][kk + (lane >> 5)][32 + (lane & 31)];
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b0, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b1, acc[1], 0, 0, 0);
+        }
+        if (s + 1 < stages) store_stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds columns j (tile 0) and j+32 (tile 1) for 16 rows.
+    const int j = lane & 31;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wave * 32 + mfma32_row(lane, r);
+        if (row >= args.m) continue;
+        const float lo = acc[0][r];
+        const float hi = acc[1][r];
+        if constexpr (E == GemmEpilogue::kStore) {
+            args.c[row * args.n + n0 + j] = lo;
+            args.c[row * args.n + n0 + 32 + j] = hi;
+        } else if constexpr (E == GemmEpilogue::kResidual) {
+            const int64_t i0 = row * args.n + n0 + j;
+            args.c[i0] = args.residual[i0] + lo;
+            args.c[i0 + 32] = args.residual[i0 + 32] + hi;
+        } else if constexpr (E == GemmEpilogue::kSwiglu) {
+            const int half = args.n / 2;
+            args.c[row * half + (n0 >> 1) + j] = silu(lo) * hi;
+        } else {  // kQkvRope: tile = one head; columns j / j+32 are the RoPE pair.
+            const int head = n0 / kHeadDim;
+            if (head < kQHeads + kKVHeads) {
+                const float* cr = args.rope_cos + row * kHeadDim;
+                const float* sr = args.rope_sin + row * kHeadDim;
+                const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
+                const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
+                float* dst = head < kQHeads
+                                 ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
+                                 : args.key_cache + (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
+                dst[j] = qlo;
+                dst[j + 32] = qhi;
+            } else {
+                float* dst = args.value_cache +
+                             (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
+                dst[j] = lo;
+                dst[j + 32] = hi;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA prefill attention.
+constexpr int kQTile = 64;
+constexpr int kKTile = 64;
+constexpr int kAttnThreads = 256;
+constexpr int kKVPad = 4;
+
+__global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const float* __restrict__ q,
+                                                                         const float* __restrict__ key_cache,
+                                                                         const float* __restrict__ value_cache,
+                                                                         int64_t seq, int64_t capacity, float scale,
+                                                                         float* __restrict__ out_rows) {
+    __shared__ float k_s[kKTile][kHeadDim + kKVPad];
+    __shared__ float v_s[kKTile][kHeadDim + kKVPad];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t q_tiles = (seq + kQTile - 1) / kQTile;
+    // Longest tiles first: block b -> q tile (q_tiles - 1 - b / 9), head b % 9.
+    const int64_t qt = q_tiles - 1 - blockIdx.x / kQHeads;
+    const int h = blockIdx.x % kQHeads;
+    const int g = h / kGroup;
+    const int64_t q0 = qt * kQTile;
+    const int64_t row_base = q0 + wave * 16;
+    const int64_t my_row = row_base + (lane & 15);  // query row of this lane in S^T / O^T layouts
+
+    // B operand of S^T = K Q^T: lane holds Q[row = lane%16][d = 4s + lane/16].
+    float qreg[16];
+    {
+        const int64_t r = my_row < seq ? my_row : seq - 1;
+        const float* qp = q + (static_cast<int64_t>(h) * seq + r) * kHeadDim;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) qreg[s] = qp[4 * s + (lane >> 4)];
+    }
+
+    const float* kg = key_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
+    const float* vg = value_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
+
+    f32x4 o_acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o_acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+
+    const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
+    const int64_t k_tiles = last_key / kKTile + 1;
+    for (int64_t kt = 0; kt < k_tiles; ++kt) {
+        const int64_t k0 = kt * kKTile;
+        __syncthreads();
+        // Stage K and V tiles (64 x 64 each): 1024 float4 per tile, 4 per thread.
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int idx = threadIdx.x + it * kAttnThreads;
+            const int row = idx >> 4;
+            const int col = (idx & 15) * 4;
+            const int64_t key = k0 + row;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (key < seq) {
+                kv = *reinterpret_cast<const float4*>(kg + key * kHeadDim + col);
+                vv = *reinterpret_cast<const float4*>(vg + key * kHeadDim + col);
+            }
+            *reinterpret_cast<float4*>(&k_s[row][col]) = kv;
+            *reinterpret_cast<float4*>(&v_s[row][col]) = vv;
+        }
+        __syncthreads();
+
+        // S^T tile: 4 key blocks of 16 x (16 rows), K-dim 64 = 16 MFMA steps.
+        f32x4 s_acc[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            s_acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const float a = k_s[kb * 16 + (lane & 15)][4 * s + (lane >> 4)];
+                s_acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qreg[s], s_acc[kb], 0, 0, 0);
+            }
+        }
+        // Scale + causal mask; lane holds keys k0 + 16kb + 4(lane/16) + r for row my_row.
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t key = k0 + 16 * kb + 4 * (lane >> 4) + r;
+                const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale : -INFINITY;
+                s_acc[kb][r] = v;
+                tile_max = fmaxf(tile_max, v);
+            }
+        }
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
+        const float m_new = fmaxf(m_run, tile_max);
+        const float alpha = m_new == -INFINITY ? 1.0f : (m_run == -INFINITY ? 0.0f : expf(m_run - m_new));
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = s_acc[kb][r] == -INFINITY ? 0.0f : expf(s_acc[kb][r] - m_new);
+                s_acc[kb][r] = p;
+                psum += p;
+            }
+        }
+        psum += __shfl_xor(psum, 16, kWave);
+        psum += __shfl_xor(psum, 32, kWave);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o_acc[db] *= alpha;
+        // O^T += V^T P^T: k-step (kb, r) uses keys 16kb + 4(lane/16) + r.
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int krow = 16 * kb + 4 * (lane >> 4) + r;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const float a = v_s[krow][16 * db + (lane & 15)];
+                    o_acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s_acc[kb][r], o_acc[db], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // O^T accumulator: lane holds d = 16db + 4(lane/16) + r for row my_row.
+    if (my_row < seq) {
+        const float inv = 1.0f / l_run;
+        float* dst = out_rows + my_row * kHidden + h * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[16 * db + 4 * (lane >> 4) + r] = o_acc[db][r] * inv;
+        }
+    }
+}
+
+__global__ void embedding_gather_kernel(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
+                                        float* hidden) {
+    const int64_t total = seq * (kHidden / 4);
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t row = i / (kHidden / 4);
+        const int64_t col = (i % (kHidden / 4)) * 4;
+        const int64_t token = ids[row];
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (token >= 0 && token < vocab) v = *reinterpret_cast<const float4*>(embedding + token * kHidden + col);
+        *reinterpret_cast<float4*>(hidden + row * kHidden + col) = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
+    if (args.k % kBK != 0 || args.n % kBN != 0 || args.m <= 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(args.n / kBN), static_cast<unsigned>((args.m + kBM - 1) / kBM));
+    switch (epilogue) {
+        case GemmEpilogue::kStore:
+            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kStore>, grid, dim3(kGemmThreads), 0, stream, args);
+            break;
+        case GemmEpilogue::kResidual:
+            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kResidual>, grid, dim3(kGemmThreads), 0, stream, args);
+            break;
+        case GemmEpilogue::kSwiglu:
+            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kSwiglu>, grid, dim3(kGemmThreads), 0, stream, args);
+            break;
+        case GemmEpilogue::kQkvRope:
+            if (args.n != kQKV) return hipErrorInvalidValue;
+            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kQkvRope>, grid, dim3(kGemmThreads), 0, stream, args);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
+                                    int64_t capacity, float scale, float* out_rows, hipStream_t stream) {
+    if (seq <= 0 || seq > capacity) return hipErrorInvalidValue;
+    const int64_t q_tiles = (seq + kQTile - 1) / kQTile;
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(q_tiles * kQHeads)), dim3(kAttnThreads), 0,
+                       stream, q, key_cache, value_cache, seq, capacity, scale, out_rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding_gather(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
+                                   float* hidden, hipStream_t stream) {
+    const int64_t total = seq * (kHidden / 4);
+    const int grid = static_cast<int>((total + 255) / 256 < 16384 ? (total + 255) / 256 : 16384);
+    hipLaunchKernelGGL(embedding_gather_kernel, dim3(grid), dim3(256), 0, stream, ids, embedding, vocab, seq, hidden);
+    return hipGetLastError();
+}
+
+}  // namespace flux

@@ -1,0 +1,549 @@
+// C++ host runtime of the MI355X SmolLM2 token loop.  See runtime.h.
+#include "runtime.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace flux {
+
+void check_hip(hipError_t status, const char* what) {
+    if (status != hipSuccess) {
+        throw FluxError(FLUX_ERROR_HIP, std::string("flux native runtime: ") + what + " failed: " +
+                                            hipGetErrorString(status));
+    }
+}
+
+namespace {
+
+[[noreturn]] void invalid(const std::string& message) { throw FluxError(FLUX_ERROR_INVALID_VALUE, message); }
+[[noreturn]] void bad_state(const std::string& message) { throw FluxError(FLUX_ERROR_STATE, message); }
+
+size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
+
+void validate_weights(const flux_weights& w, const char* who) {
+    if (w.vocab_size <= 0) invalid(std::string(who) + ": vocabulary must be non-empty");
+    if (w.embedding == nullptr || w.lm_head == nullptr || w.final_norm == nullptr)
+        invalid(std::string(who) + ": embedding, LM-head and final norm weights are required");
+    for (int i = 0; i < kLayers; ++i) {
+        if (!w.input_norm[i] || !w.packed_qkv[i] || !w.o_proj[i] || !w.post_norm[i] || !w.gate_up[i] || !w.down[i])
+            invalid(std::string(who) + ": exactly 30 complete layer descriptors are required");
+    }
+}
+
+void validate_scalars(const double* epsilons, const double* scales, const char* who) {
+    if (epsilons == nullptr || scales == nullptr) invalid(std::string(who) + ": epsilons and scales are required");
+    for (int i = 0; i < kLayers; ++i) {
+        if (!std::isfinite(epsilons[i]) || epsilons[i] <= 0.0)
+            invalid(std::string(who) + ": every RMSNorm epsilon must be positive");
+        if (!std::isfinite(scales[i])) invalid(std::string(who) + ": every attention scale must be finite");
+    }
+}
+
+int decode_grid() {
+    const int cus = device_cu_count();
+    int blocks = 0;
+    check_hip(fused_decode_occupancy(&blocks), "querying fused decode occupancy");
+    if (blocks < 1) throw FluxError(FLUX_ERROR_HIP, "flux native decode: fused decode kernel cannot be resident");
+    // One workgroup per CU; every workgroup must be co-resident (they exchange data).
+    return std::min(cus, 3 * kMaxAttnChunks);
+}
+
+}  // namespace
+
+int device_cu_count() {
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    int cus = 0;
+    check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device), "querying CU count");
+    return cus;
+}
+
+// ---------------------------------------------------------------------------
+// DecodeRuntime
+
+DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos, const float* rope_sin,
+                             int64_t capacity, int64_t position, const int64_t* initial_token,
+                             const CacheSources& sources, const double* epsilons, const double* scales,
+                             hipStream_t stream)
+    : capacity_(capacity), start_position_(position), weights_(weights), rope_cos_(rope_cos), rope_sin_(rope_sin) {
+    validate_weights(weights, "flux native full decode");
+    validate_scalars(epsilons, scales, "flux native full decode");
+    if (capacity < 1 || capacity > kMaxCapacity)
+        invalid("flux native full decode: cache capacity must be in [1, " + std::to_string(kMaxCapacity) + "]");
+    if (position < 0 || position >= capacity)
+        invalid("flux native full decode: initial position must be inside capacity");
+    if (rope_cos == nullptr || rope_sin == nullptr) invalid("flux native full decode: RoPE tables are required");
+    if (initial_token == nullptr) invalid("flux native full decode: initial token is required");
+    if (position > 0 && (sources.keys == nullptr || sources.values == nullptr || sources.lengths == nullptr))
+        invalid("flux native full decode: reset requires one K/V tensor per layer");
+    vocab_ = weights.vocab_size;
+    final_eps_ = static_cast<float>(epsilons[0]);
+    check_hip(hipGetDevice(&device_), "hipGetDevice");
+    grid_ = decode_grid();
+    if (capacity_ > max_attention_positions(grid_))
+        invalid("flux native full decode: capacity exceeds what the fused attention split can hold on this device");
+
+    try {
+        allocate();
+        std::vector<LayerWeights> host_layers(kLayers);
+        for (int i = 0; i < kLayers; ++i) {
+            host_layers[i] = LayerWeights{weights.input_norm[i], weights.packed_qkv[i], weights.o_proj[i],
+                                          weights.post_norm[i], weights.gate_up[i], weights.down[i],
+                                          static_cast<float>(epsilons[i]), static_cast<float>(scales[i])};
+        }
+        check_hip(hipMemcpyAsync(layers_, host_layers.data(), sizeof(LayerWeights) * kLayers, hipMemcpyHostToDevice,
+                                 stream),
+                  "uploading layer descriptors");
+        check_hip(hipMemsetAsync(ll_, 0, ll_bytes_, stream), "clearing exchange arena");
+        check_hip(hipMemsetAsync(token_counter_, 0, sizeof(uint32_t), stream), "clearing token counter");
+        check_hip(hipMemsetAsync(error_, 0, sizeof(int32_t), stream), "clearing error word");
+
+        args_ = DecodeArgs{layers_, weights.embedding, weights.lm_head, weights.final_norm, final_eps_,
+                           rope_cos_, rope_sin_, key_cache_, value_cache_, logits_, input_token_, generated_,
+                           generation_step_, position_, cache_length_, ll_, token_counter_, error_, capacity_,
+                           vocab_, capacity_, 1};
+
+        check_hip(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking), "creating capture stream");
+        check_hip(hipEventCreateWithFlags(&completion_, hipEventDisableTiming), "creating completion event");
+
+        // Warm the step once (as the reference does before capture), then restore state.
+        initialize_state(initial_token, sources, position, stream, false);
+        hipEvent_t setup = nullptr;
+        check_hip(hipEventCreateWithFlags(&setup, hipEventDisableTiming), "creating setup event");
+        check_hip(hipEventRecord(setup, stream), "recording setup event");
+        check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
+        check_hip(launch_fused_decode(args_, grid_, capture_stream_), "warming fused decode");
+        check_hip(hipStreamSynchronize(capture_stream_), "warming fused decode");
+        check_hip(hipEventDestroy(setup), "destroying setup event");
+        if (device_error() != 0) throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: warm-up step failed");
+        initialize_state(initial_token, sources, position, capture_stream_, true);
+        check_hip(hipStreamSynchronize(capture_stream_), "initialising decode state");
+
+        // Capture one token step (a single fused-kernel node) for replay().
+        check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
+        hipError_t launch_status = launch_fused_decode(args_, grid_, capture_stream_);
+        hipGraph_t graph = nullptr;
+        hipError_t end_status = hipStreamEndCapture(capture_stream_, &graph);
+        graph_ = graph;
+        check_hip(launch_status, "capturing fused decode step");
+        check_hip(end_status, "ending graph capture");
+        check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating decode graph");
+        check_hip(hipStreamSynchronize(capture_stream_), "finalising capture");
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+DecodeRuntime::~DecodeRuntime() { release(); }
+
+void DecodeRuntime::release() noexcept {
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(device_);
+    if (pending_ && completion_ != nullptr) (void)hipEventSynchronize(completion_);
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    if (completion_) (void)hipEventDestroy(completion_);
+    if (capture_stream_) {
+        (void)hipStreamSynchronize(capture_stream_);
+        (void)hipStreamDestroy(capture_stream_);
+    }
+    if (cache_block_) (void)hipFree(cache_block_);
+    if (state_block_) (void)hipFree(state_block_);
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+    completion_ = nullptr;
+    capture_stream_ = nullptr;
+    cache_block_ = state_block_ = nullptr;
+    if (previous >= 0 && previous != device_) (void)hipSetDevice(previous);
+}
+
+void DecodeRuntime::allocate() {
+    const size_t cache_elems = static_cast<size_t>(kLayers) * kKVHeads * capacity_ * kHeadDim;
+    check_hip(hipMalloc(&cache_block_, 2 * cache_elems * sizeof(float)), "allocating K/V cache");
+    key_cache_ = static_cast<float*>(cache_block_);
+    value_cache_ = key_cache_ + cache_elems;
+
+    ll_bytes_ = ll_arena_words() * sizeof(uint64_t);
+    size_t offset = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = offset;
+        offset = align_up(offset + bytes, 256);
+        return at;
+    };
+    const size_t o_logits = take(sizeof(float) * vocab_);
+    const size_t o_token = take(sizeof(int64_t));
+    const size_t o_generated = take(sizeof(int64_t) * capacity_);
+    const size_t o_step = take(sizeof(int64_t));
+    const size_t o_position = take(sizeof(int64_t));
+    const size_t o_length = take(sizeof(int64_t));
+    const size_t o_counter = take(sizeof(uint32_t));
+    const size_t o_error = take(sizeof(int32_t));
+    const size_t o_layers = take(sizeof(LayerWeights) * kLayers);
+    const size_t o_ll = take(ll_bytes_);
+    state_bytes_ = offset;
+    check_hip(hipMalloc(&state_block_, state_bytes_), "allocating decode state");
+    char* base = static_cast<char*>(state_block_);
+    logits_ = reinterpret_cast<float*>(base + o_logits);
+    input_token_ = reinterpret_cast<int64_t*>(base + o_token);
+    generated_ = reinterpret_cast<int64_t*>(base + o_generated);
+    generation_step_ = reinterpret_cast<int64_t*>(base + o_step);
+    position_ = reinterpret_cast<int64_t*>(base + o_position);
+    cache_length_ = reinterpret_cast<int64_t*>(base + o_length);
+    token_counter_ = reinterpret_cast<uint32_t*>(base + o_counter);
+    error_ = reinterpret_cast<int32_t*>(base + o_error);
+    layers_ = reinterpret_cast<LayerWeights*>(base + o_layers);
+    ll_ = reinterpret_cast<uint64_t*>(base + o_ll);
+}
+
+void DecodeRuntime::initialize_state(const int64_t* token, const CacheSources& sources, int64_t position,
+                                     hipStream_t stream, bool clear_outputs) {
+    const size_t cache_bytes = static_cast<size_t>(kLayers) * kKVHeads * capacity_ * kHeadDim * sizeof(float);
+    check_hip(hipMemsetAsync(key_cache_, 0, cache_bytes, stream), "clearing K cache");
+    check_hip(hipMemsetAsync(value_cache_, 0, cache_bytes, stream), "clearing V cache");
+    if (position > 0) {
+        const size_t row_bytes = static_cast<size_t>(position) * kHeadDim * sizeof(float);
+        const size_t dst_pitch = static_cast<size_t>(capacity_) * kHeadDim * sizeof(float);
+        for (int i = 0; i < kLayers; ++i) {
+            const size_t src_pitch = static_cast<size_t>(sources.lengths[i]) * kHeadDim * sizeof(float);
+            const size_t layer_offset = static_cast<size_t>(i) * kKVHeads * capacity_ * kHeadDim;
+            check_hip(hipMemcpy2DAsync(key_cache_ + layer_offset, dst_pitch, sources.keys[i], src_pitch, row_bytes,
+                                       kKVHeads, hipMemcpyDeviceToDevice, stream),
+                      "importing K cache");
+            check_hip(hipMemcpy2DAsync(value_cache_ + layer_offset, dst_pitch, sources.values[i], src_pitch, row_bytes,
+                                       kKVHeads, hipMemcpyDeviceToDevice, stream),
+                      "importing V cache");
+        }
+    }
+    check_hip(launch_install_state(token, position, 0, false, input_token_, position_, cache_length_, generation_step_,
+                                   generated_, stream),
+              "initialising device state");
+    if (clear_outputs) {
+        check_hip(hipMemsetAsync(logits_, 0, sizeof(float) * vocab_, stream), "clearing logits");
+        check_hip(hipMemsetAsync(generated_, 0, sizeof(int64_t) * capacity_, stream), "clearing generated tokens");
+    }
+}
+
+float* DecodeRuntime::replay(const int64_t* token, hipStream_t stream) {
+    if (replay_count_ >= capacity_ - start_position_)
+        bad_state("flux native full decode: fixed-capacity state is exhausted");
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering consecutive replays");
+    if (token != nullptr)
+        check_hip(hipMemcpyAsync(input_token_, token, sizeof(int64_t), hipMemcpyDeviceToDevice, stream),
+                  "copying replay token");
+    check_hip(hipGraphLaunch(graph_exec_, stream), "launching decode graph");
+    check_hip(hipEventRecord(completion_, stream), "recording replay completion");
+    pending_ = true;
+    ++replay_count_;
+    return logits_;
+}
+
+void DecodeRuntime::launch_steps(int64_t steps, hipStream_t stream, hipStream_t) {
+    DecodeArgs args = args_;
+    // One launch runs many tokens; keep launches bounded so a single kernel stays short.
+    constexpr int64_t kMaxStepsPerLaunch = 1024;
+    for (int64_t done = 0; done < steps; done += kMaxStepsPerLaunch) {
+        args.steps = static_cast<int>(std::min(kMaxStepsPerLaunch, steps - done));
+        check_hip(launch_fused_decode(args, grid_, stream), "launching fused decode");
+    }
+}
+
+int64_t* DecodeRuntime::generate_greedy(int64_t decode_steps, hipStream_t stream, float* elapsed_ms) {
+    if (decode_steps < 0)
+        invalid("flux native full decode: generation step count must be non-negative");
+    if (decode_steps > capacity_ - start_position_ - replay_count_)
+        bad_state("flux native full decode: fixed-capacity generation is exhausted");
+    if (generation_started_) bad_state("flux native full decode: prefill or reset is required before reuse");
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering greedy generation");
+    if (decode_steps > 0) {
+        hipEvent_t start = nullptr, stop = nullptr;
+        if (elapsed_ms != nullptr) {
+            check_hip(hipEventCreate(&start), "creating timing event");
+            check_hip(hipEventCreate(&stop), "creating timing event");
+            check_hip(hipEventRecord(start, stream), "recording timing event");
+        }
+        launch_steps(decode_steps, stream, stream);
+        if (elapsed_ms != nullptr) {
+            check_hip(hipEventRecord(stop, stream), "recording timing event");
+            check_hip(hipEventSynchronize(stop), "waiting for timing event");
+            check_hip(hipEventElapsedTime(elapsed_ms, start, stop), "reading timing events");
+            (void)hipEventDestroy(start);
+            (void)hipEventDestroy(stop);
+        }
+        check_hip(hipEventRecord(completion_, stream), "recording generation completion");
+        pending_ = true;
+        replay_count_ += decode_steps;
+    }
+    generation_started_ = true;
+    return generated_;
+}
+
+void DecodeRuntime::reset(const int64_t* token, const CacheSources& sources, int64_t position, hipStream_t stream) {
+    if (token == nullptr) invalid("flux native full decode: token is required");
+    if (position < 0 || position >= capacity_)
+        invalid("flux native full decode: reset position must be inside capacity");
+    if (position > 0 && (sources.keys == nullptr || sources.values == nullptr || sources.lengths == nullptr))
+        invalid("flux native full decode: reset requires one K/V tensor per layer");
+    if (position > 0) {
+        for (int i = 0; i < kLayers; ++i) {
+            if (sources.keys[i] == nullptr || sources.values[i] == nullptr || sources.lengths[i] < position)
+                invalid("flux native full decode: every K/V source must be contiguous float32 "
+                        "[1, 3, sequence>=position, 64]");
+        }
+    }
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) {
+        check_hip(hipEventSynchronize(completion_), "waiting to reset full runtime");
+        pending_ = false;
+    }
+    initialize_state(token, sources, position, stream, true);
+    check_hip(hipStreamSynchronize(stream), "resetting full runtime state");
+    start_position_ = position;
+    replay_count_ = 0;
+    generation_started_ = false;
+}
+
+void DecodeRuntime::wait_for_prefill(hipStream_t stream) {
+    if (pending_) {
+        check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering prefill after decode work");
+        pending_ = false;
+    }
+}
+
+void DecodeRuntime::install_prefilled_state(const int64_t* token, int64_t position, hipStream_t stream) {
+    if (position < 1 || position > capacity_)
+        invalid("flux native full decode: prefill position must be in [1, capacity]");
+    check_hip(launch_install_state(token, position, 1, true, input_token_, position_, cache_length_, generation_step_,
+                                   generated_, stream),
+              "installing prefilled state");
+    check_hip(hipEventRecord(completion_, stream), "recording prefill completion");
+    start_position_ = position;
+    replay_count_ = 0;
+    generation_started_ = false;
+    pending_ = true;
+}
+
+int64_t DecodeRuntime::read_scalar(const int64_t* device_value) {
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting to inspect runtime state");
+    int64_t result = -1;
+    check_hip(hipMemcpy(&result, device_value, sizeof(result), hipMemcpyDeviceToHost), "reading device state");
+    int32_t err = 0;
+    check_hip(hipMemcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
+    if (err != 0)
+        throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: device-side error " + std::to_string(err) +
+                                               (err == 1 ? " (cross-workgroup wait timed out)"
+                                                         : " (position outside capacity)"));
+    return result;
+}
+
+int32_t DecodeRuntime::device_error() {
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting for runtime");
+    int32_t err = 0;
+    check_hip(hipMemcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
+    return err;
+}
+
+void DecodeRuntime::buffers(flux_decode_buffers* out) const {
+    std::memset(out, 0, sizeof(*out));
+    out->input_token = input_token_;
+    out->logits = logits_;
+    out->generated_tokens = generated_;
+    out->generation_step = generation_step_;
+    out->key_cache = key_cache_;
+    out->value_cache = value_cache_;
+    out->position = position_;
+    out->cache_length = cache_length_;
+    out->workspace = ll_;
+    const size_t parity_words = ll_arena_words() / 2;
+    out->hidden_a = ll_;
+    out->hidden_b = ll_ + parity_words;
+    out->final_norm_output = ll_ + parity_words / 2;
+    out->attention_workspace = ll_ + parity_words / 4;
+    out->capacity = capacity_;
+    out->vocab_size = vocab_;
+    out->workspace_bytes = static_cast<int64_t>(ll_bytes_);
+    out->cache_bytes = static_cast<int64_t>(2) * kLayers * kKVHeads * capacity_ * kHeadDim * sizeof(float);
+    out->stable_buffer_bytes = static_cast<int64_t>(sizeof(int64_t) * (5 + capacity_) + sizeof(float) * vocab_);
+}
+
+// ---------------------------------------------------------------------------
+// PrefillRuntime
+
+PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_cos, const float* rope_sin,
+                               int64_t capacity, const int64_t* input_ids, int64_t sequence_length,
+                               const double* epsilons, const double* scales, hipStream_t stream)
+    : seq_(sequence_length), capacity_(capacity), weights_(weights), rope_cos_(rope_cos), rope_sin_(rope_sin) {
+    validate_weights(weights, "flux native prefill");
+    validate_scalars(epsilons, scales, "flux native prefill");
+    if (capacity < 1 || capacity > kMaxCapacity)
+        invalid("flux native prefill: cache capacity must be in [1, " + std::to_string(kMaxCapacity) + "]");
+    if (sequence_length < 1 || sequence_length > capacity)
+        invalid("flux native prefill: prompt length must be in [1, capacity]");
+    if (input_ids == nullptr || rope_cos == nullptr || rope_sin == nullptr)
+        invalid("flux native prefill: input_ids and RoPE tables are required");
+    vocab_ = weights.vocab_size;
+    for (int i = 0; i < kLayers; ++i) {
+        eps_.push_back(static_cast<float>(epsilons[i]));
+        scales_.push_back(static_cast<float>(scales[i]));
+    }
+    check_hip(hipGetDevice(&device_), "hipGetDevice");
+    lm_grid_ = std::max(1, device_cu_count());
+
+    const int64_t s = seq_;
+    size_t offset = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = offset;
+        offset = align_up(offset + bytes, 256);
+        return at;
+    };
+    const size_t o_a = take(sizeof(float) * s * kHidden);
+    const size_t o_b = take(sizeof(float) * s * kHidden);
+    const size_t o_norm = take(sizeof(float) * s * kHidden);
+    const size_t o_q = take(sizeof(float) * s * kQHeads * kHeadDim);
+    const size_t o_attn = take(sizeof(float) * s * kHidden);
+    const size_t o_swiglu = take(sizeof(float) * s * kInter);
+    const size_t o_final = take(sizeof(float) * kHidden);
+    const size_t o_logits = take(sizeof(float) * vocab_);
+    const size_t o_token = take(sizeof(int64_t));
+    const size_t o_pv = take(sizeof(float) * lm_grid_);
+    const size_t o_pi = take(sizeof(int64_t) * lm_grid_);
+    block_bytes_ = offset;
+
+    // An empty-cache decode runtime at position 0 with a zero token.
+    int64_t* zero_token = nullptr;
+    check_hip(hipMalloc(&block_, block_bytes_), "allocating prefill workspace");
+    char* base = static_cast<char*>(block_);
+    hidden_a_ = reinterpret_cast<float*>(base + o_a);
+    hidden_b_ = reinterpret_cast<float*>(base + o_b);
+    norm_ = reinterpret_cast<float*>(base + o_norm);
+    query_ = reinterpret_cast<float*>(base + o_q);
+    attn_rows_ = reinterpret_cast<float*>(base + o_attn);
+    swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
+    final_hidden_ = reinterpret_cast<float*>(base + o_final);
+    logits_ = reinterpret_cast<float*>(base + o_logits);
+    initial_token_ = reinterpret_cast<int64_t*>(base + o_token);
+    part_v_ = reinterpret_cast<float*>(base + o_pv);
+    part_i_ = reinterpret_cast<int64_t*>(base + o_pi);
+    try {
+        zero_token = initial_token_;
+        check_hip(hipMemsetAsync(zero_token, 0, sizeof(int64_t), stream), "initialising decode token");
+        decode_ = std::make_unique<DecodeRuntime>(weights, rope_cos, rope_sin, capacity, 0, zero_token,
+                                                  CacheSources{}, epsilons, scales, stream);
+        prefill(input_ids, stream);
+    } catch (...) {
+        decode_.reset();
+        (void)hipFree(block_);
+        block_ = nullptr;
+        throw;
+    }
+}
+
+PrefillRuntime::~PrefillRuntime() {
+    if (decode_) {
+        try {
+            (void)decode_->device_error();
+        } catch (...) {
+        }
+    }
+    decode_.reset();
+    if (block_) (void)hipFree(block_);
+}
+
+float* PrefillRuntime::prefill(const int64_t* input_ids, hipStream_t stream) {
+    if (input_ids == nullptr) invalid("flux native prefill: input_ids are required");
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    decode_->wait_for_prefill(stream);
+    run(input_ids, stream);
+    decode_->install_prefilled_state(initial_token_, seq_, stream);
+    return logits_;
+}
+
+void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
+    flux_decode_buffers db;
+    decode_->buffers(&db);
+    check_hip(launch_embedding_gather(input_ids, weights_.embedding, vocab_, seq_, hidden_a_, stream),
+              "launching embedding gather");
+    const int64_t layer_elems = static_cast<int64_t>(kKVHeads) * capacity_ * kHeadDim;
+    for (int layer = 0; layer < kLayers; ++layer) {
+        float* keys = db.key_cache + layer * layer_elems;
+        float* values = db.value_cache + layer * layer_elems;
+        check_hip(launch_rmsnorm_rows(hidden_a_, weights_.input_norm[layer], norm_, seq_, kHidden, eps_[layer], stream),
+                  "launching input RMSNorm");
+        GemmArgs qkv{};
+        qkv.a = norm_;
+        qkv.b = weights_.packed_qkv[layer];
+        qkv.m = seq_;
+        qkv.n = kQKV;
+        qkv.k = kHidden;
+        qkv.rope_cos = rope_cos_;
+        qkv.rope_sin = rope_sin_;
+        qkv.q_out = query_;
+        qkv.key_cache = keys;
+        qkv.value_cache = values;
+        qkv.capacity = capacity_;
+        check_hip(launch_gemm(qkv, GemmEpilogue::kQkvRope, stream), "launching QKV GEMM");
+        check_hip(launch_prefill_attention(query_, keys, values, seq_, capacity_, scales_[layer], attn_rows_, stream),
+                  "launching prefill attention");
+        GemmArgs o{};
+        o.a = attn_rows_;
+        o.b = weights_.o_proj[layer];
+        o.c = hidden_b_;
+        o.residual = hidden_a_;
+        o.m = seq_;
+        o.n = kHidden;
+        o.k = kHidden;
+        check_hip(launch_gemm(o, GemmEpilogue::kResidual, stream), "launching o_proj GEMM");
+        check_hip(launch_rmsnorm_rows(hidden_b_, weights_.post_norm[layer], norm_, seq_, kHidden, eps_[layer], stream),
+                  "launching post-attention RMSNorm");
+        GemmArgs gu{};
+        gu.a = norm_;
+        gu.b = weights_.gate_up[layer];
+        gu.c = swiglu_;
+        gu.m = seq_;
+        gu.n = kGateUp;
+        gu.k = kHidden;
+        check_hip(launch_gemm(gu, GemmEpilogue::kSwiglu, stream), "launching gate/up GEMM");
+        GemmArgs dn{};
+        dn.a = swiglu_;
+        dn.b = weights_.down[layer];
+        dn.c = hidden_a_;
+        dn.residual = hidden_b_;
+        dn.m = seq_;
+        dn.n = kHidden;
+        dn.k = kInter;
+        check_hip(launch_gemm(dn, GemmEpilogue::kResidual, stream), "launching down GEMM");
+    }
+    const float* last_row = hidden_a_ + (seq_ - 1) * kHidden;
+    check_hip(launch_rmsnorm_rows(last_row, weights_.final_norm, final_hidden_, 1, kHidden, eps_[0], stream),
+              "launching final RMSNorm");
+    check_hip(launch_lm_head_argmax(final_hidden_, nullptr, 0.0f, weights_.lm_head, vocab_, logits_, part_v_, part_i_,
+                                    lm_grid_, initial_token_, stream),
+              "launching LM head + argmax");
+}
+
+int64_t* PrefillRuntime::generate_greedy(int64_t max_new_tokens, hipStream_t stream) {
+    if (max_new_tokens < 1) invalid("flux native prefill: max_new_tokens must be positive");
+    if (max_new_tokens > capacity_ - seq_ + 1)
+        bad_state("flux native prefill: generation exceeds fixed cache capacity");
+    return decode_->generate_greedy(max_new_tokens - 1, stream);
+}
+
+void PrefillRuntime::buffers(flux_prefill_buffers* out) const {
+    std::memset(out, 0, sizeof(*out));
+    out->prefill_logits = logits_;
+    out->prefill_workspace = block_;
+    out->attention_output = attn_rows_;
+    out->final_hidden = final_hidden_;
+    out->initial_token = initial_token_;
+    out->sequence_length = seq_;
+    out->capacity = capacity_;
+    out->workspace_bytes = static_cast<int64_t>(block_bytes_);
+}
+
+}  // namespace flux

@@ -1,0 +1,275 @@
+/*
+ * flux_amd.h -- C ABI of the MI355X-native (gfx950) SmolLM2 FP32 token loop.
+ *
+ * Drop-in boundary for Flux's native path.  The reference binds the same
+ * functionality as PyTorch custom classes and CUDA launchers; every entry point
+ * below names the reference interface it replaces (paths are relative to the
+ * reference repository).  Plain pointers and sizes only: device pointers are
+ * hipMalloc'd (or torch-allocated) device memory, streams are hipStream_t, and
+ * nothing here depends on PyTorch.
+ *
+ * Conventions
+ *  - Every function returns FLUX_OK (0) or an error code; flux_last_error()
+ *    returns the calling thread's message for the last failure.  Invalid
+ *    arguments are rejected before any launch (reference launchers return
+ *    cudaErrorInvalidValue, e.g. csrc/packed_gate_up_gemv/packed_gate_up_gemv_cuda.cu:57-59).
+ *  - Launches are asynchronous on the given stream and never allocate, except
+ *    the runtime constructors, which own their buffers (as the reference's
+ *    at::empty allocations in native_decode_runtime_cuda.cu:1162-1224).
+ *  - Weights are borrowed: the caller keeps them alive for the runtime's life
+ *    (the reference holds refcounted tensors, native_decode_runtime_cuda.cu:796-805).
+ *  - Geometry is fixed to SmolLM2-135M: 30 layers, hidden 576, intermediate
+ *    1536, 9 query heads, 3 KV heads, head_dim 64.  Vocabulary and capacity are
+ *    runtime values; capacity may be up to FLUX_MAX_CAPACITY (the reference caps
+ *    at 8192, native_decode_runtime_cuda.cu:36).
+ */
+#ifndef FLUX_AMD_H_
+#define FLUX_AMD_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FLUX_LAYERS 30
+#define FLUX_HIDDEN 576
+#define FLUX_INTERMEDIATE 1536
+#define FLUX_QUERY_HEADS 9
+#define FLUX_KV_HEADS 3
+#define FLUX_HEAD_DIM 64
+#define FLUX_PACKED_QKV_WIDTH 960
+#define FLUX_PACKED_GATE_UP_WIDTH 3072
+#define FLUX_MAX_CAPACITY 16384
+
+enum flux_status {
+    FLUX_OK = 0,
+    FLUX_ERROR_INVALID_VALUE = 1, /* bad pointer / size / shape */
+    FLUX_ERROR_HIP = 2,           /* a HIP runtime call failed */
+    FLUX_ERROR_STATE = 3,         /* capacity exhausted, reuse without prefill/reset */
+    FLUX_ERROR_DEVICE = 4         /* a kernel reported a device-side error */
+};
+
+/* Borrowed model weights (row-major float32, device memory).
+ * Mirrors the tensor arguments of NativeSmolLM2Decode / NativeSmolLM2Prefill
+ * (csrc/native_decode_runtime/native_decode_runtime.h:59-77,
+ *  csrc/native_prefill_runtime/native_prefill_runtime.h:16-31). */
+typedef struct flux_weights {
+    const float* embedding;                   /* [vocab, 576] */
+    const float* lm_head;                     /* [vocab, 576] (tied: may equal embedding) */
+    const float* final_norm;                  /* [576] */
+    const float* input_norm[FLUX_LAYERS];     /* [576] */
+    const float* packed_qkv[FLUX_LAYERS];     /* [960, 576] = cat(q, k, v) */
+    const float* o_proj[FLUX_LAYERS];         /* [576, 576] */
+    const float* post_norm[FLUX_LAYERS];      /* [576] */
+    const float* gate_up[FLUX_LAYERS];        /* [3072, 576] = cat(gate, up) */
+    const float* down[FLUX_LAYERS];           /* [576, 1536] */
+    int64_t vocab_size;
+} flux_weights;
+
+typedef struct flux_decode flux_decode;
+typedef struct flux_prefill flux_prefill;
+
+/* Stable runtime-owned device buffers (NativeSmolLM2Decode::addresses(),
+ * native_decode_runtime_cuda.cu:1490-1505, and the tensor accessors :1470-1488). */
+typedef struct flux_decode_buffers {
+    int64_t* input_token;      /* [1] */
+    float* logits;             /* [vocab] */
+    int64_t* generated_tokens; /* [capacity] */
+    int64_t* generation_step;  /* [1] */
+    float* key_cache;          /* [30, 1, 3, capacity, 64] */
+    float* value_cache;        /* [30, 1, 3, capacity, 64] */
+    int64_t* position;         /* [1] */
+    int64_t* cache_length;     /* [1] */
+    void* workspace;           /* exchange arena of the fused decode kernel */
+    void* hidden_a;            /* layer-output exchange words, even layers */
+    void* hidden_b;            /* layer-output exchange words, odd layers */
+    void* final_norm_output;   /* argmax exchange words */
+    void* attention_workspace; /* attention partial exchange words */
+    int64_t capacity;
+    int64_t vocab_size;
+    int64_t workspace_bytes;
+    int64_t cache_bytes;
+    int64_t stable_buffer_bytes;
+} flux_decode_buffers;
+
+typedef struct flux_prefill_buffers {
+    float* prefill_logits;          /* [vocab] */
+    void* prefill_workspace;        /* activation slab */
+    float* attention_output;        /* [S, 576] attention rows */
+    float* final_hidden;            /* [576] final-norm output of the last row */
+    int64_t* initial_token;         /* [1] prefill argmax */
+    int64_t sequence_length;
+    int64_t capacity;
+    int64_t workspace_bytes;
+} flux_prefill_buffers;
+
+/* Thread-local message for the last failing call ("" if none). */
+const char* flux_last_error(void);
+
+/* Version string of this library. */
+const char* flux_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Decode runtime: replaces torch.classes.flux.NativeSmolLM2Decode
+ * (csrc/native_decode_runtime/native_decode_runtime.h:57-119,
+ *  native_decode_runtime_cuda.cu:742-865; registered in
+ *  native_decode_runtime_torch.cpp:38-79).
+ * key_sources/value_sources: per layer [1, 3, source_lengths[i], 64] contiguous
+ * float32 with source_lengths[i] >= position; may be NULL when position == 0.
+ * Builds the stable buffers, imports the cache, and captures one decode step in
+ * a hipGraph.  `stream` orders the setup (the reference's current stream). */
+int flux_decode_create(const flux_weights* weights, const float* rope_cos, const float* rope_sin, int64_t capacity,
+                       int64_t position, const int64_t* initial_token, const float* const* key_sources,
+                       const float* const* value_sources, const int64_t* source_lengths, const double* epsilons,
+                       const double* attention_scales, hipStream_t stream, flux_decode** out);
+
+/* One decode step: optional token copy (device [1,1] int64, may be NULL), then
+ * graph replay; returns the logits buffer.  (native_decode_runtime_cuda.cu:907-931) */
+int flux_decode_replay(flux_decode* runtime, const int64_t* token, hipStream_t stream, float** logits);
+
+/* `decode_steps` greedy steps in one launch of the fused decode kernel; returns
+ * the generated-token buffer.  (native_decode_runtime_cuda.cu:933-960) */
+int flux_decode_generate_greedy(flux_decode* runtime, int64_t decode_steps, hipStream_t stream,
+                                int64_t** generated_tokens);
+
+/* Synchronously restore token, cache and position.  (native_decode_runtime_cuda.cu:962-981) */
+int flux_decode_reset(flux_decode* runtime, const int64_t* token, const float* const* key_sources,
+                      const float* const* value_sources, const int64_t* source_lengths, int64_t position,
+                      hipStream_t stream);
+
+/* Synchronising scalar reads (read_scalar, native_decode_runtime_cuda.cu:1029-1040).
+ * They also surface device-side errors as FLUX_ERROR_DEVICE. */
+int flux_decode_position(flux_decode* runtime, int64_t* out);
+int flux_decode_cache_length(flux_decode* runtime, int64_t* out);
+int flux_decode_generation_step(flux_decode* runtime, int64_t* out);
+int flux_decode_replay_count(const flux_decode* runtime, int64_t* out);
+int flux_decode_capacity(const flux_decode* runtime, int64_t* out);
+int flux_decode_get_buffers(const flux_decode* runtime, flux_decode_buffers* out);
+/* Wait for outstanding work and return the device error word (0 = none). */
+int flux_decode_device_error(flux_decode* runtime, int32_t* out);
+/* Time the next `decode_steps` steps with events on `stream` (benchmark aid). */
+int flux_decode_generate_greedy_timed(flux_decode* runtime, int64_t decode_steps, hipStream_t stream,
+                                      float* milliseconds);
+void flux_decode_destroy(flux_decode* runtime);
+
+/* ------------------------------------------------------------------------ */
+/* Prefill runtime: replaces torch.classes.flux.NativeSmolLM2Prefill
+ * (csrc/native_prefill_runtime/native_prefill_runtime.h:14-60,
+ *  native_prefill_runtime_cuda.cu:355-445; registered in
+ *  native_prefill_runtime_torch.cpp:5-45).  Creates its own decode runtime with
+ * an empty cache, runs the prompt (input_ids: device [1, S] int64) and hands the
+ * compact cache to the decode runtime without a copy. */
+int flux_prefill_create(const flux_weights* weights, const float* rope_cos, const float* rope_sin, int64_t capacity,
+                        const int64_t* input_ids, int64_t sequence_length, const double* epsilons,
+                        const double* attention_scales, hipStream_t stream, flux_prefill** out);
+
+/* Re-run the fixed-shape prompt and re-install the decode state
+ * (native_prefill_runtime_cuda.cu:540-551). */
+int flux_prefill_run(flux_prefill* runtime, const int64_t* input_ids, hipStream_t stream, float** logits);
+
+/* max_new_tokens tokens: the prefill argmax plus max_new_tokens-1 decode steps
+ * (native_prefill_runtime_cuda.cu:738-746). */
+int flux_prefill_generate_greedy(flux_prefill* runtime, int64_t max_new_tokens, hipStream_t stream,
+                                 int64_t** generated_tokens);
+
+/* The attached decode runtime (owned by the prefill runtime). */
+flux_decode* flux_prefill_decode(flux_prefill* runtime);
+int flux_prefill_get_buffers(const flux_prefill* runtime, flux_prefill_buffers* out);
+void flux_prefill_destroy(flux_prefill* runtime);
+
+/* ------------------------------------------------------------------------ */
+/* Per-kernel launchers (isolated kernels of the token loop). */
+
+/* rows x cols RMSNorm: out = w * (x * rsqrt(mean(x^2) + eps)).
+ * Replaces rmsnorm_cuda_fp32 (csrc/rmsnorm/rmsnorm_cuda.h:9-19). */
+int flux_rmsnorm_f32(const float* x, const float* weight, float* out, int64_t rows, int64_t cols, float eps,
+                     hipStream_t stream);
+
+/* residual_out = hidden + residual; norm_out = rmsnorm(residual_out).
+ * Replaces residual_rmsnorm_cuda_fp32 (csrc/residual_rmsnorm/residual_rmsnorm_cuda.cu:108-150). */
+int flux_residual_rmsnorm_f32(const float* hidden, const float* residual, const float* weight, float* norm_out,
+                              float* residual_out, int64_t rows, int64_t cols, float eps, hipStream_t stream);
+
+/* Decode QKV step fused: rmsnorm(hidden) -> packed QKV GEMV [960,576] -> RoPE at
+ * *position -> q_out [9,64]; K/V written to key/value cache [3, capacity, 64] row
+ * *position.  Replaces the cuBLASLt QKV GEMV (native_decode_runtime_cuda.cu:213-218)
+ * plus packed_qkv_rope_cache_at_position_cuda_fp32 (packed_qkv_rope_cache_cuda.cu:153-179). */
+int flux_qkv_rope_cache_f32(const float* hidden, const float* norm_weight, float eps, const float* packed_qkv,
+                            const float* rope_cos, const float* rope_sin, const int64_t* position, int64_t capacity,
+                            float* key_cache, float* value_cache, float* q_out, hipStream_t stream);
+
+/* One-token GQA attention over compact K/V [3, capacity, 64] for positions
+ * [0, *position] with split-K partials in `workspace`.
+ * Replaces gqa_decode_attention_cuda_fp32 (csrc/gqa_decode_attention/gqa_decode_attention_cuda.cu:551-633). */
+int flux_gqa_decode_workspace_bytes(int64_t capacity, int64_t* bytes);
+int flux_gqa_decode_attention_f32(const float* q, const float* key_cache, const float* value_cache,
+                                  const int64_t* position, int64_t capacity, float scale, void* workspace,
+                                  int64_t workspace_bytes, float* out, hipStream_t stream);
+
+/* out[rows] = W[rows, 576] x[576] (+ residual[rows] if non-NULL).
+ * Replaces the cuBLASLt o_proj GEMV (native_decode_runtime_cuda.cu:271-276) and
+ * residual add. */
+int flux_linear576_f32(const float* x, const float* weight, const float* residual, float* out, int64_t rows,
+                       hipStream_t stream);
+
+/* out[1536] = silu(Wg x) * (Wu x), x = rmsnorm(hidden) when norm_weight != NULL.
+ * Replaces packed_gate_up_swiglu_cuda_fp32 (csrc/packed_gate_up_gemv/packed_gate_up_gemv_cuda.cu:25-63). */
+int flux_gate_up_swiglu_f32(const float* hidden, const float* norm_weight, float eps, const float* packed_gate_up,
+                            float* out, hipStream_t stream);
+
+/* out[576] = residual + W_down[576,1536] s.  Replaces cublasSgemm + cublasSgeam
+ * (native_decode_runtime_cuda.cu:290-309). */
+int flux_down_residual_f32(const float* s, const float* down, const float* residual, float* out, hipStream_t stream);
+
+/* logits = lm_head x (x = rmsnorm(hidden) when norm_weight != NULL) and the
+ * exact lowest-index argmax into *token.  Replaces the lm_head cublasSgemm
+ * (native_decode_runtime_cuda.cu:1078-1087) + greedy_argmax_cuda_fp32. */
+int flux_lm_head_workspace_bytes(int64_t* bytes);
+int flux_lm_head_argmax_f32(const float* hidden, const float* norm_weight, float eps, const float* lm_head,
+                            int64_t vocab, float* logits, int64_t* token, void* workspace, int64_t workspace_bytes,
+                            hipStream_t stream);
+
+/* Greedy argmax (greedy_generation_cuda.cu:99-132): lowest index of the
+ * maximum, NaN counts as maximum.  The _update form also writes
+ * generated[*step] = token, *step += 1, *position = *attention_length. */
+int flux_greedy_argmax_f32(const float* logits, int64_t vocab, int64_t* token, hipStream_t stream);
+int flux_greedy_argmax_update_f32(const float* logits, int64_t vocab, int64_t* input_token, int64_t* generated_tokens,
+                                  int64_t* generation_step, int64_t generated_capacity, int64_t* position,
+                                  const int64_t* attention_length, hipStream_t stream);
+
+/* Prefill linear on FP32 MFMA: C[m,n] = A[m,k] W[n,k]^T (+ residual[m,n]).
+ * Replaces linear_fp32 / cublasSgemm (native_prefill_runtime_cuda.cu:285-302).
+ * n % 64 == 0, k % 16 == 0. */
+int flux_linear_f32(const float* a, const float* weight, const float* residual, float* c, int64_t m, int64_t n,
+                    int64_t k, hipStream_t stream);
+
+/* Prefill gate/up GEMM with SwiGLU epilogue: out[m,1536] = silu(x Wg^T) * (x Wu^T).
+ * Replaces linear_fp32 + packed_swiglu_cuda_fp32 (csrc/packed_swiglu/packed_swiglu_cuda.cu:35-56). */
+int flux_gate_up_swiglu_rows_f32(const float* x, const float* packed_gate_up, float* out, int64_t rows,
+                                 hipStream_t stream);
+
+/* Prefill QKV GEMM with RoPE epilogue for positions 0..rows-1: q_out [9,rows,64],
+ * K/V cache rows [3, capacity, 64].  Replaces linear_fp32 +
+ * packed_qkv_rope_cache_prefill_fp32_kernel (native_prefill_runtime_cuda.cu:124-163). */
+int flux_qkv_rope_cache_rows_f32(const float* x, const float* packed_qkv, const float* rope_cos, const float* rope_sin,
+                                 int64_t rows, float* q_out, float* key_cache, float* value_cache, int64_t capacity,
+                                 hipStream_t stream);
+
+/* Causal GQA prefill attention (FP32 MFMA, online softmax): q [9,seq,64], K/V
+ * [3,capacity,64] -> out_rows [seq, 576].  Replaces streaming_prefill_gqa_cuda_fp32
+ * (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu:423-460) + K15. */
+int flux_prefill_attention_f32(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
+                               int64_t capacity, float scale, float* out_rows, hipStream_t stream);
+
+/* hidden[s] = embedding[ids[s]] (zero row when out of vocabulary).
+ * Replaces embedding_gather_fp32_kernel (native_prefill_runtime_cuda.cu:85-103). */
+int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq, float* hidden,
+                              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLUX_AMD_H_ */

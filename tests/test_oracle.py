@@ -1,0 +1,239 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+* OracleLlama vs the golden vectors written from transformers' LlamaForCausalLM.
+* Per-kernel closed forms vs known answers, brute force, HF fixtures and the
+  reference's own C++ CPU implementations (oracle/_ref, built from
+  /root/reference/csrc by oracle/Makefile when the reference is present).
+* Planted mistakes (in the oracle, on the CPU) must fail these checks.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from flux_amd import synthetic
+from oracle import kernels as ref
+from oracle import llama_fp32
+from oracle.llama_fp32 import OracleCache, OracleConfig, OracleLlama, rope_table
+from tests.conftest import GOLDEN, ROOT, golden
+
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libfluxref.so")
+
+
+@pytest.fixture(scope="module")
+def small_oracle() -> OracleLlama:
+    return OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128)))
+
+
+@pytest.fixture(scope="module")
+def smol_oracle() -> OracleLlama:
+    return OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=0)))
+
+
+def test_synthetic_weights_are_reproducible():
+    with open(os.path.join(GOLDEN, "weights.json")) as handle:
+        meta = json.load(handle)
+    small = synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128))
+    assert synthetic.weights_sha256(small) == meta["weights_seed2701_vocab128"]
+    full = synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=0))
+    assert synthetic.weights_sha256(full) == meta["weights_seed0_vocab49152"]
+    assert full["lm_head.weight"] is full["model.embed_tokens.weight"]
+    emb = full["model.embed_tokens.weight"]
+    assert emb.shape == (49152, 576) and abs(float(emb.std()) - 0.02) < 2e-4
+
+
+def test_prompts_are_reproducible():
+    record = golden("config1.npz")
+    assert synthetic.synthetic_prompt(1, 128)[0].numpy().tolist() == record["prompt"].tolist()
+    ids = synthetic.synthetic_prompt(2, 512)
+    assert int(ids.min()) >= 0 and int(ids.max()) < 49152
+
+
+def _probe_check(logits: torch.Tensor, record: dict, step: int, atol: float = 1e-5) -> None:
+    top_idx = torch.from_numpy(record["top_indices"][step])
+    torch.testing.assert_close(logits[top_idx], torch.from_numpy(record["top_values"][step]), atol=atol, rtol=1e-5)
+    probe_idx = torch.from_numpy(record["probe_indices"])
+    probe_idx = probe_idx[probe_idx < logits.numel()]
+    torch.testing.assert_close(logits[probe_idx], torch.from_numpy(record["probe"][step]), atol=atol, rtol=1e-5)
+
+
+def test_oracle_matches_hf_small_vocab(small_oracle):
+    record = golden("small128.npz")
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0)
+    tokens, logits, cache = small_oracle.greedy(prompt, len(record["tokens"]), keep_logits=True)
+    assert tokens == record["tokens"].tolist()
+    for step, row in enumerate(logits):
+        _probe_check(row, record, step)
+
+
+def test_oracle_matches_hf_config1(smol_oracle):
+    record = golden("config1.npz")
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0)
+    tokens, logits, cache = smol_oracle.greedy(prompt, 8, keep_logits=True)
+    assert tokens == record["tokens"][:8].tolist()
+    for step, row in enumerate(logits):
+        _probe_check(row, record, step)
+    # K/V after the prompt (positions recorded by the golden script).
+    positions = torch.from_numpy(record["kv_positions"])
+    for layer in (0, 15, 29):
+        k = cache.keys[layer][0][:, positions]
+        torch.testing.assert_close(k, torch.from_numpy(record[f"k{layer}"]), rtol=1e-5, atol=1e-6)
+
+
+def test_rope_table_matches_hf_rotary_embedding():
+    record = golden("rope.npz")
+    cos, sin = rope_table(OracleConfig(), 8704)
+    assert hashlib.sha256(cos.numpy().tobytes()).digest() == record["cos_sha256"].tobytes()
+    assert hashlib.sha256(sin.numpy().tobytes()).digest() == record["sin_sha256"].tobytes()
+    rows = torch.from_numpy(record["rows"])
+    assert torch.equal(cos[rows], torch.from_numpy(record["cos"]))
+
+
+def test_rope_rows_bit_exact_vs_hf_apply_rotary():
+    record = golden("ops.npz")
+    cos = torch.from_numpy(record["rope_cos"])[:, None]  # [1,1,5,64]
+    sin = torch.from_numpy(record["rope_sin"])[:, None]
+    q_embed = ref.rope_rows(torch.from_numpy(record["rope_q"]), cos, sin)
+    k_embed = ref.rope_rows(torch.from_numpy(record["rope_k"]), cos, sin)
+    assert torch.equal(q_embed, torch.from_numpy(record["rope_q_embed"]))  # rtol=atol=0, test_references.py:321-331
+    assert torch.equal(k_embed, torch.from_numpy(record["rope_k_embed"]))
+
+
+def test_rope_identity_kat():
+    x = torch.randn(3, 64, generator=torch.Generator().manual_seed(5))
+    assert torch.equal(ref.rope_rows(x, torch.ones(64), torch.zeros(64)), x)
+
+
+def test_rmsnorm_known_answer_and_hf():
+    out = ref.rmsnorm(torch.tensor([[3.0, 4.0]]), torch.tensor([2.0, 0.5]), 0.0)
+    torch.testing.assert_close(out, torch.tensor([[6 / 12.5 ** 0.5, 2 / 12.5 ** 0.5]], dtype=torch.float64))
+    record = golden("ops.npz")
+    out = ref.rmsnorm(torch.from_numpy(record["norm_x"]), torch.from_numpy(record["norm_w"]), 1e-5)
+    torch.testing.assert_close(out.float(), torch.from_numpy(record["norm_y"]), rtol=1e-5, atol=1e-6)
+
+
+def test_greedy_argmax_kats():
+    v = np.zeros(1000, dtype=np.float32)
+    v[177] = v[321] = 5.0
+    assert ref.greedy_argmax(v) == 177
+    v = np.full(64, -1.0, dtype=np.float32)
+    v[19] = v[27] = 2.0
+    assert ref.greedy_argmax(v) == 19
+    assert ref.greedy_argmax(np.full(10, -np.inf, dtype=np.float32)) == 0
+    assert ref.greedy_argmax(np.asarray([1.0, np.nan, 3.0, np.nan], dtype=np.float32)) == 1
+    x = np.random.default_rng(0).standard_normal(4096).astype(np.float32)
+    assert ref.greedy_argmax(x) == int(torch.argmax(torch.from_numpy(x)))
+
+
+def test_gqa_decode_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(9, 64, generator=g)
+    k = torch.randn(3, 40, 64, generator=g)
+    v = torch.randn(3, 40, 64, generator=g)
+    # Single attended position -> that V row, for every head of the group.
+    out = ref.gqa_decode_attention(q, k, v, 1, 0.125)
+    torch.testing.assert_close(out, v[:, 0].double().repeat_interleave(3, dim=0))
+    # Zero query -> mean of V rows.
+    out = ref.gqa_decode_attention(torch.zeros(9, 64), k, v, 33, 0.125)
+    torch.testing.assert_close(out, v[:, :33].double().mean(1).repeat_interleave(3, dim=0))
+    # Agreement with torch's softmax attention with repeat_kv.
+    out = ref.gqa_decode_attention(q, k, v, 40, 0.125)
+    kk = k.repeat_interleave(3, dim=0).double()
+    vv = v.repeat_interleave(3, dim=0).double()
+    p = torch.softmax((kk @ q.double()[:, :, None])[..., 0] * 0.125, dim=-1)
+    torch.testing.assert_close(out, (p[:, None, :] @ vv)[:, 0])
+
+
+def test_causal_attention_closed_forms():
+    g = torch.Generator().manual_seed(4)
+    k = torch.randn(3, 20, 64, generator=g)
+    v = torch.randn(3, 20, 64, generator=g)
+    out = ref.causal_attention(torch.zeros(9, 20, 64), k, v, 0.125)
+    prefix = v.double().cumsum(1) / torch.arange(1, 21).double()[None, :, None]
+    torch.testing.assert_close(out, prefix.repeat_interleave(3, dim=0))
+    q = torch.randn(9, 20, 64, generator=g)
+    out = ref.causal_attention(q, k, v, 0.125)
+    for h in range(9):  # row 0 attends only to key 0
+        torch.testing.assert_close(out[h, 0], v[h // 3, 0].double())
+
+
+def test_gate_up_swiglu_closed_form():
+    x = torch.tensor([1.0, -2.0])
+    w = torch.tensor([[1.0, 0.0], [0.0, 1.0], [2.0, 0.0], [0.0, 3.0]])  # gate rows then up rows
+    out = ref.gate_up_swiglu(x, w)
+    g = torch.tensor([1.0, -2.0], dtype=torch.float64)
+    u = torch.tensor([2.0, -6.0], dtype=torch.float64)
+    torch.testing.assert_close(out, g * torch.sigmoid(g) * u)
+
+
+def test_algorithmic_byte_and_flop_models():
+    # B(L) and F(S) of the measurement model (weights 538,060,032 B; per-position 46,080 B).
+    assert ref.decode_bytes_per_token(0) == 538_060_032 + 2_304 + 46_080
+    assert ref.decode_bytes_per_token(8192) == 538_060_032 + 2_304 + 46_080 * 8193
+    assert ref.prefill_flops(1) == 212_336_640 + 34_560 * 2 + 56_623_104
+    assert abs(ref.prefill_flops(8192) - 4.059e12) < 1e9
+
+
+@pytest.mark.skipif(not os.path.exists(REF_LIB), reason="oracle/_ref not built (needs /root/reference)")
+def test_oracle_against_reference_cpu_sources():
+    lib = ctypes.CDLL(REF_LIB)
+    fp = ctypes.POINTER(ctypes.c_float)
+    L, F = ctypes.c_long, ctypes.c_float
+    lib.ref_rmsnorm.argtypes = [fp, fp, fp, L, L, F]
+    lib.ref_residual_rmsnorm.argtypes = [fp, fp, fp, fp, fp, L, L, F]
+    lib.ref_packed_swiglu.argtypes = [fp, fp, L, L]
+    lib.ref_rope.argtypes = [fp, fp, fp, fp, fp, fp, L, L, L, L]
+
+    def p(t):
+        return t.numpy().ctypes.data_as(fp)
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(4, 576, generator=g)
+    w = torch.randn(576, generator=g)
+    out = torch.empty(4, 576)
+    assert lib.ref_rmsnorm(p(x), p(w), p(out), 4, 576, ctypes.c_float(1e-5)) == 0
+    torch.testing.assert_close(out.double(), ref.rmsnorm(x, w, 1e-5), rtol=1e-5, atol=1e-6)
+    r = torch.randn(4, 576, generator=g)
+    norm, res = torch.empty(4, 576), torch.empty(4, 576)
+    assert lib.ref_residual_rmsnorm(p(x), p(r), p(w), p(norm), p(res), 4, 576, ctypes.c_float(1e-5)) == 0
+    en, er = ref.residual_rmsnorm(x, r, w, 1e-5)
+    assert torch.equal(res, er)
+    torch.testing.assert_close(norm.double(), en, rtol=1e-5, atol=1e-6)
+    packed = torch.randn(3, 2 * 1536, generator=g)
+    sw = torch.empty(3, 1536)
+    assert lib.ref_packed_swiglu(p(packed), p(sw), 3, 1536) == 0
+    gg, uu = packed[:, :1536].double(), packed[:, 1536:].double()
+    torch.testing.assert_close(sw.double(), gg * torch.sigmoid(gg) * uu, rtol=1e-5, atol=1e-6)
+    # RoPE: the reference's un-fused rounding equals ours bit for bit.
+    q = torch.randn(9, 5, 64, generator=g)
+    k = torch.randn(3, 5, 64, generator=g)
+    cos, sin = rope_table(OracleConfig(), 5)
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    assert lib.ref_rope(p(q), p(k), p(cos), p(sin), p(qo), p(ko), 9, 3, 5, 64) == 0
+    assert torch.equal(qo, ref.rope_rows(q, cos, sin))
+    assert torch.equal(ko, ref.rope_rows(k, cos, sin))
+
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    """Mutations of the oracle (wrong RoPE sign, transposed attention operand) fail the pins."""
+    record = golden("ops.npz")
+    cos = torch.from_numpy(record["rope_cos"])[:, None]
+    sin = torch.from_numpy(record["rope_sin"])[:, None]
+    q = torch.from_numpy(record["rope_q"])
+    half = 32
+    wrong = q * cos + torch.cat((q[..., half:], -q[..., :half]), dim=-1) * sin
+    assert not torch.equal(wrong, torch.from_numpy(record["rope_q_embed"]))
+    monkeypatch.setattr(llama_fp32, "rotate_half", lambda x: torch.cat((x[..., x.shape[-1] // 2:],
+                                                                          -x[..., :x.shape[-1] // 2]), dim=-1))
+    small = OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128)))
+    rec = golden("small128.npz")
+    logits = small.forward(torch.from_numpy(rec["prompt"]).unsqueeze(0), OracleCache())[0, -1]
+    with pytest.raises(AssertionError):
+        _probe_check(logits, rec, 0)
