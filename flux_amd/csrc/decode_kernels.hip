@@ -35,10 +35,20 @@
 namespace flux {
 namespace {
 
+// threadIdx.x read through an empty asm so that per-lane address arithmetic is
+// recomputed where it is used instead of being hoisted out of the token/layer
+// loops by LICM; hoisted lane-dependent values otherwise exhaust the VGPR budget
+// of the persistent kernel and spill to scratch.
+__device__ __forceinline__ unsigned tid_opaque() {
+    unsigned t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 constexpr int kThreads = 512;
 constexpr int kWavesPerWG = kThreads / kWave;
 constexpr int kPosSlots = kThreads / 16;  // attention: 16 lanes (4 dims each) per position
-constexpr int kAttnMaxIter = 8;           // positions per WG <= kPosSlots * kAttnMaxIter = 256
+constexpr int kAttnMaxIter = 7;           // positions per WG <= kPosSlots * kAttnMaxIter = 224
 constexpr int kLmBatch = 8;
 constexpr uint64_t kTimeoutTicks = 20ull * 1000 * 1000;  // 200 ms of the 100 MHz wall clock
 
@@ -78,14 +88,30 @@ __device__ __forceinline__ void ll_fetch(const uint64_t* __restrict__ base, cons
 #pragma unroll
     for (int j = 0; j < N; ++j) ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
     if (!ready) {
+        // Two staggered polls are kept in flight so a newly published word is seen
+        // about half a memory round trip sooner than with one poll at a time.
         const uint64_t start = wall_clock64();
         while (true) {
             if (*w.abort) break;
-            __builtin_amdgcn_s_sleep(1);
+            uint64_t first[N], second[N];
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                first[j] = static_cast<uint32_t>(word[j] >> 32) == epoch ? word[j] : ll_load(base + idx[j]);
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                second[j] = static_cast<uint32_t>(word[j] >> 32) == epoch ? word[j] : ll_load(base + idx[j]);
             ready = true;
 #pragma unroll
             for (int j = 0; j < N; ++j) {
-                if (static_cast<uint32_t>(word[j] >> 32) != epoch) word[j] = ll_load(base + idx[j]);
+                if (static_cast<uint32_t>(first[j] >> 32) == epoch) word[j] = first[j];
+                ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
+            }
+            if (ready) break;
+            ready = true;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                if (static_cast<uint32_t>(second[j] >> 32) == epoch) word[j] = second[j];
                 ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
             }
             if (ready) break;
@@ -147,6 +173,22 @@ __device__ __forceinline__ float fetch_one(const In& in, int i) {
     return v[0];
 }
 
+// Normalised 576-slice with the norm weights already in registers.
+__device__ __forceinline__ void norm_slice_w(const float (&h)[9], const float (&wn)[9], float eps, float (&x)[9]) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) ss = fmaf(h[j], h[j], ss);
+    ss = wave_sum(ss);
+    const float inv = rms_inverse(ss, kHidden, eps);
+#pragma unroll
+    for (int j = 0; j < 9; ++j) x[j] = wn[j] * (h[j] * inv);
+}
+
+__device__ __forceinline__ void load_slice576(const float* __restrict__ v, int lane, float (&out)[9]) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) out[j] = v[slice576_index(lane, j)];
+}
+
 // Normalised 576-slice x = w * (h * inv_rms) with the sum of squares over the
 // whole vector (wave reduction, identical in every lane).
 __device__ __forceinline__ void norm_slice(const float (&h)[9], const float* __restrict__ weight, float eps,
@@ -199,11 +241,21 @@ __device__ __forceinline__ void qkv_load(const float* __restrict__ qkv_w, int un
 
 // Computes the unit's two rows and routes them: q -> q_out[h*64+d], k -> cache
 // (and kv_out), v -> cache (and kv_out).  Lane 0 writes.
+struct RopePair {
+    float c_lo, s_lo, c_hi, s_hi;
+};
+
+__device__ __forceinline__ RopePair rope_pair(const float* __restrict__ cos_row, const float* __restrict__ sin_row,
+                                              int unit) {
+    const int d = unit & 31;
+    return RopePair{cos_row[d], sin_row[d], cos_row[d + 32], sin_row[d + 32]};
+}
+
 template <class QOut>
-__device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float (&x)[9], int unit, int lane,
-                                           const float* __restrict__ cos_row, const float* __restrict__ sin_row,
-                                           float* __restrict__ key_row_base, float* __restrict__ value_row_base,
-                                           int64_t head_stride, const QOut& out) {
+__device__ __forceinline__ void qkv_finish_rp(const QkvUnitWeights& w, const float (&x)[9], int unit, int lane,
+                                              const RopePair& rp, float* __restrict__ key_row_base,
+                                              float* __restrict__ value_row_base, int64_t head_stride,
+                                              const QOut& out) {
     int head, d, r0, r1;
     qkv_unit_rows(unit, head, d, r0, r1);
     const float a = wave_sum(dot_lane<9>(x, w.w0));
@@ -211,8 +263,8 @@ __device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float 
     if (lane != 0) return;
     float lo, hi;
     if (head < kQHeads + kKVHeads) {
-        lo = rope_first(a, b, cos_row[d], sin_row[d]);
-        hi = rope_second(b, a, cos_row[d + 32], sin_row[d + 32]);
+        lo = rope_first(a, b, rp.c_lo, rp.s_lo);
+        hi = rope_second(b, a, rp.c_hi, rp.s_hi);
     } else {
         lo = a;
         hi = b;
@@ -229,6 +281,14 @@ __device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float 
     out.put(r1, hi);
 }
 
+template <class QOut>
+__device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float (&x)[9], int unit, int lane,
+                                           const float* __restrict__ cos_row, const float* __restrict__ sin_row,
+                                           float* __restrict__ key_row_base, float* __restrict__ value_row_base,
+                                           int64_t head_stride, const QOut& out) {
+    qkv_finish_rp(w, x, unit, lane, rope_pair(cos_row, sin_row, unit), key_row_base, value_row_base, head_stride, out);
+}
+
 // ---------------------------------------------------------------------------
 // Phase B: attention partial for (KV group g, chunk c) over positions
 // [begin, end).  Positions < `current` come from the cache (prefetched before the
@@ -238,12 +298,27 @@ __device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float 
 struct AttnChunk {
     float4 k[kAttnMaxIter];
     float4 v[kAttnMaxIter];
+    __device__ __forceinline__ float4 key(int i, int64_t, int) const { return k[i]; }
+    __device__ __forceinline__ float4 value(int i, int64_t, int) const { return v[i]; }
+};
+
+// LDS-staged rows of the fused kernel (row r = pos - begin).
+struct AttnLdsRows {
+    const float* k_lds;
+    const float* v_lds;
+    int64_t begin;
+    __device__ __forceinline__ float4 key(int, int64_t pos, int quad) const {
+        return *reinterpret_cast<const float4*>(k_lds + (pos - begin) * kHeadDim + 4 * quad);
+    }
+    __device__ __forceinline__ float4 value(int, int64_t pos, int quad) const {
+        return *reinterpret_cast<const float4*>(v_lds + (pos - begin) * kHeadDim + 4 * quad);
+    }
 };
 
 __device__ __forceinline__ void attn_prefetch(const float* __restrict__ key_cache_g, const float* __restrict__ value_cache_g,
                                               int64_t begin, int64_t end, int64_t current, AttnChunk& ch) {
-    const int slot = threadIdx.x >> 4;
-    const int quad = threadIdx.x & 15;
+    const int slot = tid_opaque() >> 4;
+    const int quad = tid_opaque() & 15;
 #pragma unroll
     for (int i = 0; i < kAttnMaxIter; ++i) {
         const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
@@ -257,36 +332,56 @@ __device__ __forceinline__ void attn_prefetch(const float* __restrict__ key_cach
     }
 }
 
+// Fused-kernel variant: stage the chunk's cached K/V rows [begin, begin + rows)
+// straight into LDS with global_load_lds_dwordx4 (no register staging).  Each
+// instruction moves 1 KB = 4 rows; wave w moves blocks w, w+8, ...
+__device__ __forceinline__ void attn_stage_lds(const float* __restrict__ key_cache_g,
+                                               const float* __restrict__ value_cache_g, int64_t begin, int rows,
+                                               float* k_lds, float* v_lds) {
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
+    const int blocks = (rows + 3) >> 2;
+    for (int b = wave; b < blocks; b += kWavesPerWG) {
+        if (4 * b + (lane >> 4) < rows) {
+            const int64_t offset = (begin + 4 * b) * kHeadDim + 4 * lane;
+            __builtin_amdgcn_global_load_lds(key_cache_g + offset, k_lds + b * 256, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(value_cache_g + offset, v_lds + b * 256, 16, 0, 0);
+        }
+    }
+}
+
 // q4[h] = query dims of this thread for the 3 heads; knew/vnew = dims of the new row.
 // red: LDS scratch of kWavesPerWG * kGroup * 66 floats.
-template <class POut>
-__device__ __forceinline__ void attn_compute(AttnChunk& ch, const float4 (&q4)[kGroup], float4 knew, float4 vnew,
+template <class Rows, class POut>
+__device__ __forceinline__ void attn_compute(Rows& ch, const float4 (&q4)[kGroup], float4 knew, float4 vnew,
                                              int64_t begin, int64_t end, int64_t current, float scale,
                                              float* red, const POut& out) {
-    const int slot = threadIdx.x >> 4;
-    const int quad = threadIdx.x & 15;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int slot = tid_opaque() >> 4;
+    const int quad = tid_opaque() & 15;
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
     float s[kGroup][kAttnMaxIter];
     float m[kGroup];
 #pragma unroll
     for (int h = 0; h < kGroup; ++h) m[h] = -INFINITY;
+    const int iters = static_cast<int>((end - begin + kPosSlots - 1) / kPosSlots);
+    const float scale2 = scale * kLog2e;  // scores in log2 units
 #pragma unroll
     for (int i = 0; i < kAttnMaxIter; ++i) {
+#pragma unroll
+        for (int h = 0; h < kGroup; ++h) s[h][i] = -INFINITY;
+        if (i >= iters) continue;
         const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
         const bool valid = pos < end;
-        if (pos == current) {
-            ch.k[i] = knew;
-            ch.v[i] = vnew;
-        }
+        const float4 kr = pos == current ? knew : ch.key(i, pos, quad);
 #pragma unroll
         for (int h = 0; h < kGroup; ++h) {
-            float part = q4[h].x * ch.k[i].x;
-            part = fmaf(q4[h].y, ch.k[i].y, part);
-            part = fmaf(q4[h].z, ch.k[i].z, part);
-            part = fmaf(q4[h].w, ch.k[i].w, part);
+            float part = q4[h].x * kr.x;
+            part = fmaf(q4[h].y, kr.y, part);
+            part = fmaf(q4[h].z, kr.z, part);
+            part = fmaf(q4[h].w, kr.w, part);
             const float dot = group_sum<16>(part);
-            s[h][i] = valid ? dot * scale : -INFINITY;
+            s[h][i] = valid ? dot * scale2 : -INFINITY;
             m[h] = fmaxf(m[h], s[h][i]);
         }
     }
@@ -319,12 +414,15 @@ __device__ __forceinline__ void attn_compute(AttnChunk& ch, const float4 (&q4)[k
         if (m[h] == -INFINITY) continue;
 #pragma unroll
         for (int i = 0; i < kAttnMaxIter; ++i) {
-            const float p = s[h][i] == -INFINITY ? 0.0f : expf(s[h][i] - m[h]);
+            if (s[h][i] == -INFINITY) continue;
+            const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
+            const float4 vr = pos == current ? vnew : ch.value(i, pos, quad);
+            const float p = fast_exp2(s[h][i] - m[h]);
             l[h] += p;
-            o[h].x = fmaf(p, ch.v[i].x, o[h].x);
-            o[h].y = fmaf(p, ch.v[i].y, o[h].y);
-            o[h].z = fmaf(p, ch.v[i].z, o[h].z);
-            o[h].w = fmaf(p, ch.v[i].w, o[h].w);
+            o[h].x = fmaf(p, vr.x, o[h].x);
+            o[h].y = fmaf(p, vr.y, o[h].y);
+            o[h].z = fmaf(p, vr.z, o[h].z);
+            o[h].w = fmaf(p, vr.w, o[h].w);
         }
     }
 #pragma unroll
@@ -348,9 +446,9 @@ __device__ __forceinline__ void attn_compute(AttnChunk& ch, const float4 (&q4)[k
     }
     __syncthreads();
     // Threads 0..191 finish (head h = t/64, dim d = t%64); thread t%64==0 also m,l.
-    if (threadIdx.x < kGroup * kHeadDim) {
-        const int h = threadIdx.x >> 6;
-        const int dim = threadIdx.x & 63;
+    if (tid_opaque() < kGroup * kHeadDim) {
+        const int h = tid_opaque() >> 6;
+        const int dim = tid_opaque() & 63;
         float acc = 0.0f;
         float lsum = 0.0f;
         for (int w = 0; w < kWavesPerWG; ++w) {
@@ -383,8 +481,8 @@ struct PartialLLOut {
 template <class In, class Out>
 __device__ __forceinline__ void merge_head(const In& in, int chunks, int64_t partial_stride, float* red,
                                            const Out& out) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
     float M = -INFINITY, L = 0.0f, O = 0.0f;
     for (int c = wave; c < chunks; c += kWavesPerWG) {
         const int base = static_cast<int>(c * partial_stride);
@@ -394,8 +492,8 @@ __device__ __forceinline__ void merge_head(const In& in, int chunks, int64_t par
         const float mc = v[1];
         if (mc == -INFINITY) continue;
         const float nm = fmaxf(M, mc);
-        const float a = M == -INFINITY ? 0.0f : expf(M - nm);
-        const float b = expf(mc - nm);
+        const float a = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+        const float b = fast_exp2(mc - nm);
         O = O * a + v[0] * b;
         L = L * a + v[2] * b;
         M = nm;
@@ -409,17 +507,17 @@ __device__ __forceinline__ void merge_head(const In& in, int chunks, int64_t par
         red_l[wave] = L;
     }
     __syncthreads();
-    if (threadIdx.x < kHeadDim) {
+    if (tid_opaque() < kHeadDim) {
         float mm = -INFINITY;
         for (int w = 0; w < kWavesPerWG; ++w) mm = fmaxf(mm, red_m[w]);
         float acc = 0.0f, lsum = 0.0f;
         for (int w = 0; w < kWavesPerWG; ++w) {
             if (red_m[w] == -INFINITY) continue;
-            const float f = expf(red_m[w] - mm);
-            acc += red_o[w * kHeadDim + threadIdx.x] * f;
+            const float f = fast_exp2(red_m[w] - mm);
+            acc += red_o[w * kHeadDim + tid_opaque()] * f;
             lsum += red_l[w] * f;
         }
-        out.put(threadIdx.x, acc / lsum);
+        out.put(tid_opaque(), acc / lsum);
     }
     __syncthreads();
 }
@@ -466,14 +564,14 @@ struct LogitsPlainOut {
 
 // Workgroup argmax reduction of per-wave (value, index); result valid in thread 0.
 __device__ __forceinline__ void wg_argmax(float& v, int64_t& i, float* red_v, int64_t* red_i) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
     if (lane == 0) {
         red_v[wave] = v;
         red_i[wave] = i;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid_opaque() == 0) {
         for (int w = 1; w < kWavesPerWG; ++w) {
             if (argmax_precedes(red_v[w], red_i[w], v, i)) {
                 v = red_v[w];
@@ -504,30 +602,80 @@ __device__ __forceinline__ uint32_t epoch_of(uint32_t token_counter, int stage) 
     return token_counter * 32u + static_cast<uint32_t>(stage) + 1u;
 }
 
+// Optional phase timestamps for latency analysis (compiled only with -DFLUX_TRACE).
+#ifdef FLUX_TRACE
+__device__ uint64_t g_flux_trace[4][kLayers + 1][16];
+__device__ uint64_t g_flux_trace_all[512][16];
+#define FLUX_TRACE_POINT(slot)                                                                         \
+    do {                                                                                               \
+        if (t == 2 && tid_opaque() == 0 && (wg % 85) == 0 && wg / 85 < 4)                              \
+            g_flux_trace[wg / 85][layer][slot] = wall_clock64();                                       \
+        if (t == 2 && layer == 15 && tid_opaque() == 0) g_flux_trace_all[wg][slot] = wall_clock64();   \
+    } while (0)
+#else
+#define FLUX_TRACE_POINT(slot) \
+    do {                       \
+    } while (0)
+#endif
+
+// ---------------------------------------------------------------------------
+// Workgroup-cooperative LL fetch into LDS.  Word k (0 <= k < count) is read from
+// base + index(k); each thread polls at most kMax words in one batch.  Threads
+// with fewer words re-poll word index(0), which belongs to the same vector.
+template <int kMax, class IndexFn>
+__device__ __forceinline__ void wg_ll_fetch(const uint64_t* __restrict__ base, int count, IndexFn index,
+                                            uint32_t epoch, const WaitCtx& w, float* lds) {
+    int idx[kMax];
+    float v[kMax];
+#pragma unroll
+    for (int j = 0; j < kMax; ++j) {
+        const int k = static_cast<int>(tid_opaque()) + j * kThreads;
+        idx[j] = index(k < count ? k : 0);
+    }
+    if (static_cast<int>(tid_opaque()) < count) ll_fetch<kMax>(base, idx, epoch, w, v);
+#pragma unroll
+    for (int j = 0; j < kMax; ++j) {
+        const int k = static_cast<int>(tid_opaque()) + j * kThreads;
+        if (k < count) lds[k] = v[j];
+    }
+}
+
+struct Contiguous {
+    __device__ __forceinline__ int operator()(int k) const { return k; }
+};
+
+// Lane slice of a 576-vector held in LDS.
+__device__ __forceinline__ void lds_slice576(const float* vec, int lane, float (&v)[9]) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) v[j] = vec[slice576_index(lane, j)];
+}
+
 // ---------------------------------------------------------------------------
 // The fused persistent decode kernel: `args.steps` greedy tokens per launch.
+// Requires gridDim.x * 8 >= 1536 (one unit per wave in every phase).
 __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs args) {
     __shared__ int abort_flag;
     __shared__ float red[kWavesPerWG * kGroup * (kHeadDim + 2)];
     __shared__ int64_t red_i[kWavesPerWG];
     __shared__ float red_v[kWavesPerWG];
     __shared__ int64_t token_shared;
-    extern __shared__ float occupancy_pad[];  // dynamic LDS only to keep one WG per CU
-    (void)occupancy_pad;
+    __shared__ float hvec[kHidden];   // layer input h (residual of C)
+    __shared__ float rvec[kHidden];   // post-attention residual r (residual of E)
+    __shared__ float vec[kInter];     // attention output / SwiGLU output / q,k,v of the group
+    extern __shared__ float part[];   // merge staging [chunks][66]; sized to keep one WG per CU
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
     const int G = gridDim.x;
     const int wg = blockIdx.x;
     const int gw = wave * G + wg;        // global wave id, interleaved across CUs
-    const int TW = G * kWavesPerWG;      // total waves
     const int chunks = G / kKVHeads < kMaxAttnChunks ? G / kKVHeads : kMaxAttnChunks;
     const int64_t cap = args.capacity;
     const int64_t head_stride = cap * kHeadDim;
     const int64_t layer_stride = kKVHeads * head_stride;
-    const int64_t partial_stride = kGroup * (kHeadDim + 2);
+    const int partial_stride = kGroup * (kHeadDim + 2);
 
-    if (threadIdx.x == 0) abort_flag = 0;
+    if (tid_opaque() == 0) abort_flag = 0;
     const uint32_t counter0 = *args.token_counter;
     int64_t token = *args.input_token;
     int64_t position = *args.position;
@@ -541,7 +689,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         __syncthreads();
         if (stop) break;
         if (position < 0 || position >= cap) {
-            if (wg == 0 && threadIdx.x == 0)
+            if (wg == 0 && tid_opaque() == 0)
                 __hip_atomic_store(args.error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -555,108 +703,200 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         for (int layer = 0; layer < kLayers; ++layer) {
             const LayerWeights Lw = args.layers[layer];
             const uint32_t ep = epoch_of(counter, layer);
-            const uint32_t ep_prev = epoch_of(counter, layer - 1);  // only used for layer > 0
             uint64_t* ll = args.ll + (layer & 1) * LLLayout::kParity;
             const uint64_t* ll_prev = args.ll + ((layer + 1) & 1) * LLLayout::kParity;
             float* key_layer = args.key_cache + layer * layer_stride;
             float* value_layer = args.value_cache + layer * layer_stride;
 
-            // ---- A: QKV ----
-            for (int unit = gw; unit < kQKV / 2; unit += TW) {
+            // ---- A: norm(h) -> QKV GEMV -> RoPE -> cache (unit = row pair, one per wave) ----
+            {
+                FLUX_TRACE_POINT(0);
+                const bool active = gw < kQKV / 2;
                 QkvUnitWeights w;
-                qkv_load(Lw.qkv, unit, lane, w);
-                float h[9], x[9];
-                if (layer == 0) {
-#pragma unroll
-                    for (int j = 0; j < 9; ++j) h[j] = token_ok ? emb_row[slice576_index(lane, j)] : 0.0f;
-                } else {
-                    fetch_slice576(LLIn{ll_prev + LLLayout::kHidden, ep_prev, wctx}, lane, h);
+                float wn[9];
+                RopePair rp{};
+                if (active) {
+                    qkv_load(Lw.qkv, gw, lane, w);
+                    load_slice576(Lw.input_norm, lane, wn);
+                    rp = rope_pair(cos_row, sin_row, gw);
                 }
-                norm_slice(h, Lw.input_norm, Lw.eps, lane, x);
-                qkv_finish(w, x, unit, lane, cos_row, sin_row, key_layer + position * kHeadDim,
-                           value_layer + position * kHeadDim, head_stride, LLOut{ll + LLLayout::kQkv, ep});
+                if (layer == 0) {
+                    for (int k = tid_opaque(); k < kHidden; k += kThreads) hvec[k] = token_ok ? emb_row[k] : 0.0f;
+                } else {
+                    wg_ll_fetch<2>(ll_prev + LLLayout::kHidden, kHidden, Contiguous{}, epoch_of(counter, layer - 1),
+                                   wctx, hvec);
+                }
+                __syncthreads();
+                FLUX_TRACE_POINT(1);
+                if (active) {
+                    float h[9], x[9];
+                    lds_slice576(hvec, lane, h);
+                    norm_slice_w(h, wn, Lw.eps, x);
+                    qkv_finish_rp(w, x, gw, lane, rp, key_layer + position * kHeadDim,
+                                  value_layer + position * kHeadDim, head_stride, LLOut{ll + LLLayout::kQkv, ep});
+                }
             }
 
-            // ---- B: attention partials ----
+            // ---- B: attention partial of (KV group g, position chunk c) ----
+            FLUX_TRACE_POINT(2);
             if (wg < kKVHeads * chunks) {
                 const int g = wg % kKVHeads;
                 const int c = wg / kKVHeads;
                 int64_t begin, end;
                 chunk_range(attended, chunks, c, begin, end);
-                AttnChunk ch;
-                attn_prefetch(key_layer + g * head_stride, value_layer + g * head_stride, begin, end, position, ch);
-                const int quad = threadIdx.x & 15;
-                const LLIn qin{ll + LLLayout::kQkv, ep, wctx};
+                const int64_t cached_end = end < position ? end : position;
+                const int cached_rows = cached_end > begin ? static_cast<int>(cached_end - begin) : 0;
+                float* k_lds = part;
+                float* v_lds = part + kAttnMaxIter * kPosSlots * kHeadDim;
+                attn_stage_lds(key_layer + g * head_stride, value_layer + g * head_stride, begin, cached_rows, k_lds,
+                               v_lds);
+                const bool has_current = position >= begin && position < end;
+                // vec[0..191] = q of heads 3g..3g+2; vec[192..319] = new k row, new v row.
+                const int qbase = g * kGroup * kHeadDim;
+                const int kbase = kQHeads * kHeadDim + g * kHeadDim;
+                wg_ll_fetch<1>(ll + LLLayout::kQkv, has_current ? kGroup * kHeadDim + 2 * kHeadDim : kGroup * kHeadDim,
+                               [=](int k) {
+                                   return k < kGroup * kHeadDim ? qbase + k
+                                                                : kbase + ((k - kGroup * kHeadDim) >> 6) *
+                                                                              (kKVHeads * kHeadDim) +
+                                                                      ((k - kGroup * kHeadDim) & 63);
+                               },
+                               ep, wctx, vec);
+                __builtin_amdgcn_s_waitcnt(0);  // LDS-direct K/V loads have landed
+                __syncthreads();
+                FLUX_TRACE_POINT(3);
+                AttnLdsRows ch{k_lds, v_lds, begin};
+                const int quad = tid_opaque() & 15;
                 float4 q4[kGroup];
 #pragma unroll
-                for (int h = 0; h < kGroup; ++h) {
-                    const int base = (g * kGroup + h) * kHeadDim + 4 * quad;
-                    const int idx[4] = {base, base + 1, base + 2, base + 3};
-                    float v[4];
-                    qin.fetch(idx, v);
-                    q4[h] = make_float4(v[0], v[1], v[2], v[3]);
-                }
+                for (int h = 0; h < kGroup; ++h)
+                    q4[h] = *reinterpret_cast<const float4*>(vec + h * kHeadDim + 4 * quad);
                 float4 knew = make_float4(0.f, 0.f, 0.f, 0.f), vnew = knew;
-                if (position >= begin && position < end) {
-                    const int kb = kQHeads * kHeadDim + g * kHeadDim + 4 * quad;
-                    const int vb = (kQHeads + kKVHeads) * kHeadDim + g * kHeadDim + 4 * quad;
-                    const int idx[8] = {kb, kb + 1, kb + 2, kb + 3, vb, vb + 1, vb + 2, vb + 3};
-                    float v[8];
-                    qin.fetch(idx, v);
-                    knew = make_float4(v[0], v[1], v[2], v[3]);
-                    vnew = make_float4(v[4], v[5], v[6], v[7]);
+                if (has_current) {
+                    knew = *reinterpret_cast<const float4*>(vec + kGroup * kHeadDim + 4 * quad);
+                    vnew = *reinterpret_cast<const float4*>(vec + kGroup * kHeadDim + kHeadDim + 4 * quad);
                 }
                 attn_compute(ch, q4, knew, vnew, begin, end, position, Lw.scale, red,
                              PartialLLOut{ll + LLLayout::kPartials + (g * chunks + c) * partial_stride, ep});
             }
 
-            // ---- B2: merge per query head ----
-            if (wg < kQHeads) {
-                const int h = wg;
+            FLUX_TRACE_POINT(4);
+            // ---- B2: merge chunk partials; WG (h, quarter) handles 16 dims of query head h ----
+            if (wg < kQHeads * 4) {
+                const int h = wg >> 2;
+                const int quarter = wg & 3;
                 const int g = h / kGroup;
                 const int hh = h % kGroup;
-                const LLIn pin{ll + LLLayout::kPartials + g * chunks * partial_stride + hh * (kHeadDim + 2), ep, wctx};
-                merge_head(pin, chunks, partial_stride, red, LLOut{ll + LLLayout::kAttnMerged + h * kHeadDim, ep});
-            }
-
-            // ---- C: o_proj + residual ----
-            for (int row = gw; row < kHidden; row += TW) {
-                float w[9], a[9];
-                load_row576(Lw.o_proj + static_cast<int64_t>(row) * kHidden, lane, w);
-                fetch_slice576(LLIn{ll + LLLayout::kAttnMerged, ep, wctx}, lane, a);
-                const float dot = wave_sum(dot_lane<9>(a, w));
-                if (lane == 0) {
-                    const float resid = layer == 0 ? (token_ok ? emb_row[row] : 0.0f)
-                                                   : fetch_one(LLIn{ll_prev + LLLayout::kHidden, ep_prev, wctx}, row);
-                    ll_store(ll + LLLayout::kResid + row, resid + dot, ep);
+                constexpr int kRun = 18;  // 16 dims + m + l per chunk
+                const uint64_t* pbase = ll + LLLayout::kPartials + g * chunks * partial_stride + hh * (kHeadDim + 2);
+                wg_ll_fetch<(kMaxAttnChunks * kRun + kThreads - 1) / kThreads>(
+                    pbase, chunks * kRun,
+                    [=](int k) {
+                        const int cc = k / kRun;
+                        const int j = k - cc * kRun;
+                        return cc * partial_stride + (j < 16 ? 16 * quarter + j : kHeadDim + (j - 16));
+                    },
+                    ep, wctx, part);
+                __syncthreads();
+                FLUX_TRACE_POINT(5);
+                // Global max of the chunk maxima: lane-strided, then wave butterfly (every wave
+                // computes the same value).
+                float M = -INFINITY;
+                for (int cc = lane; cc < chunks; cc += kWave) M = fmaxf(M, part[cc * kRun + 16]);
+                M = wave_max(M);
+                // Thread (slot = t / 16, d = t % 16) sums chunks cc = slot, slot + 32, ...
+                const int d = tid_opaque() & 15;
+                const int slot = tid_opaque() >> 4;
+                float O = 0.0f, L = 0.0f;
+                for (int cc = slot; cc < chunks; cc += kThreads / 16) {
+                    const float* pc = part + cc * kRun;
+                    const float mc = pc[16];
+                    if (mc == -INFINITY) continue;
+                    const float f = fast_exp2(mc - M);
+                    O = fmaf(pc[d], f, O);
+                    L = fmaf(pc[17], f, L);
                 }
+                // Reduce over the 4 slots of a wave (lanes with equal d), then over waves.
+                O += __shfl_xor(O, 16, kWave);
+                O += __shfl_xor(O, 32, kWave);
+                L += __shfl_xor(L, 16, kWave);
+                L += __shfl_xor(L, 32, kWave);
+                if (lane < 16) {
+                    red[wave * 16 + lane] = O;
+                    red[kWavesPerWG * 16 + wave * 16 + lane] = L;
+                }
+                __syncthreads();
+                if (tid_opaque() < 16) {
+                    float acc = 0.0f, lsum = 0.0f;
+                    for (int w = 0; w < kWavesPerWG; ++w) {
+                        acc += red[w * 16 + tid_opaque()];
+                        lsum += red[kWavesPerWG * 16 + w * 16 + tid_opaque()];
+                    }
+                    ll_store(ll + LLLayout::kAttnMerged + h * kHeadDim + 16 * quarter + tid_opaque(), acc / lsum, ep);
+                }
+                __syncthreads();
             }
 
-            // ---- D: norm -> gate/up -> SwiGLU ----
-            for (int j = gw; j < kInter; j += TW) {
-                float wg_[9], wu[9], r[9], x[9];
-                load_row576(Lw.gate_up + static_cast<int64_t>(j) * kHidden, lane, wg_);
-                load_row576(Lw.gate_up + static_cast<int64_t>(kInter + j) * kHidden, lane, wu);
-                fetch_slice576(LLIn{ll + LLLayout::kResid, ep, wctx}, lane, r);
-                norm_slice(r, Lw.post_norm, Lw.eps, lane, x);
-                const float gsum = wave_sum(dot_lane<9>(x, wg_));
-                const float usum = wave_sum(dot_lane<9>(x, wu));
-                if (lane == 0) ll_store(ll + LLLayout::kSwiglu + j, silu(gsum) * usum, ep);
+            // ---- C: o_proj + residual (row = gw) ----
+            {
+                FLUX_TRACE_POINT(6);
+                const bool active = gw < kHidden;
+                float w[9];
+                if (active) load_row576(Lw.o_proj + static_cast<int64_t>(gw) * kHidden, lane, w);
+                wg_ll_fetch<2>(ll + LLLayout::kAttnMerged, kHidden, Contiguous{}, ep, wctx, vec);
+                __syncthreads();
+                FLUX_TRACE_POINT(7);
+                if (active) {
+                    float a[9];
+                    lds_slice576(vec, lane, a);
+                    const float dot = wave_sum(dot_lane<9>(a, w));
+                    if (lane == 0) ll_store(ll + LLLayout::kResid + gw, hvec[gw] + dot, ep);
+                }
+                __syncthreads();
             }
 
-            // ---- E: down + residual ----
-            for (int row = gw; row < kHidden; row += TW) {
-                float w[24], s[24];
-                load_row1536(Lw.down + static_cast<int64_t>(row) * kInter, lane, w);
-                int idx[24];
+            // ---- D: norm(r) -> gate/up GEMV -> SwiGLU (unit j = gw) ----
+            {
+                const bool active = gw < kInter;
+                float wg_[9], wu[9], wn[9];
+                if (active) {
+                    load_row576(Lw.gate_up + static_cast<int64_t>(gw) * kHidden, lane, wg_);
+                    load_row576(Lw.gate_up + static_cast<int64_t>(kInter + gw) * kHidden, lane, wu);
+                    load_slice576(Lw.post_norm, lane, wn);
+                }
+                FLUX_TRACE_POINT(8);
+                wg_ll_fetch<2>(ll + LLLayout::kResid, kHidden, Contiguous{}, ep, wctx, rvec);
+                __syncthreads();
+                FLUX_TRACE_POINT(9);
+                if (active) {
+                    float r[9], x[9];
+                    lds_slice576(rvec, lane, r);
+                    norm_slice_w(r, wn, Lw.eps, x);
+                    const float gsum = wave_sum(dot_lane<9>(x, wg_));
+                    const float usum = wave_sum(dot_lane<9>(x, wu));
+                    if (lane == 0) ll_store(ll + LLLayout::kSwiglu + gw, silu(gsum) * usum, ep);
+                }
+                __syncthreads();
+                FLUX_TRACE_POINT(12);
+            }
+
+            // ---- E: down GEMV + residual (row = gw) ----
+            {
+                const bool active = gw < kHidden;
+                float w[24];
+                if (active) load_row1536(Lw.down + static_cast<int64_t>(gw) * kInter, lane, w);
+                FLUX_TRACE_POINT(10);
+                wg_ll_fetch<3>(ll + LLLayout::kSwiglu, kInter, Contiguous{}, ep, wctx, vec);
+                __syncthreads();
+                FLUX_TRACE_POINT(11);
+                if (active) {
+                    float sv[24];
 #pragma unroll
-                for (int j = 0; j < 24; ++j) idx[j] = slice1536_index(lane, j);
-                LLIn{ll + LLLayout::kSwiglu, ep, wctx}.fetch(idx, s);
-                const float dot = wave_sum(dot_lane<24>(s, w));
-                if (lane == 0) {
-                    const float resid = fetch_one(LLIn{ll + LLLayout::kResid, ep, wctx}, row);
-                    ll_store(ll + LLLayout::kHidden + row, resid + dot, ep);
+                    for (int j = 0; j < 24; ++j) sv[j] = vec[slice1536_index(lane, j)];
+                    const float dot = wave_sum(dot_lane<24>(sv, w));
+                    if (lane == 0) ll_store(ll + LLLayout::kHidden + gw, rvec[gw] + dot, ep);
                 }
+                __syncthreads();
             }
         }
 
@@ -666,34 +906,66 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             const uint32_t ep_arg = epoch_of(counter, kLayers);
             const uint64_t* ll_last = args.ll + ((kLayers - 1) & 1) * LLLayout::kParity;
             uint64_t* ll_arg = args.ll + (t & 1) * LLLayout::kParity + LLLayout::kArgmax;
+            const int TW = G * kWavesPerWG;
             const int64_t per = (args.vocab + TW - 1) / TW;
             const int64_t row0 = per * gw < args.vocab ? per * gw : args.vocab;
             const int64_t row1 = row0 + per < args.vocab ? row0 + per : args.vocab;
+            const int layer = kLayers;
+            FLUX_TRACE_POINT(0);
+            // The first kLmPrefetch rows of this wave are loaded before waiting for h.
+            constexpr int kLmPrefetch = 8;
+            float wl[kLmPrefetch][9];
+            float wn[9];
+            load_slice576(args.final_norm, lane, wn);
+#pragma unroll
+            for (int r = 0; r < kLmPrefetch; ++r) {
+                const int64_t row = row0 + r < row1 ? row0 + r : (row1 > row0 ? row1 - 1 : 0);
+                load_row576(args.lm_head + row * kHidden, lane, wl[r]);
+            }
+            wg_ll_fetch<2>(ll_last + LLLayout::kHidden, kHidden, Contiguous{}, ep_last, wctx, hvec);
+            __syncthreads();
+            FLUX_TRACE_POINT(1);
             float h[9], x[9];
-            fetch_slice576(LLIn{ll_last + LLLayout::kHidden, ep_last, wctx}, lane, h);
-            norm_slice(h, args.final_norm, args.final_eps, lane, x);
+            lds_slice576(hvec, lane, h);
+            norm_slice_w(h, wn, args.final_eps, x);
             float best_v = -INFINITY;
             int64_t best_i = INT64_MAX;
-            lm_rows(args.lm_head, x, row0, row1, lane, LogitsPlainOut{args.logits}, best_v, best_i);
+#pragma unroll
+            for (int r = 0; r < kLmPrefetch; ++r) {
+                const float v = wave_sum(dot_lane<9>(x, wl[r]));
+                const int64_t row = row0 + r;
+                if (row < row1) {
+                    if (lane == 0) args.logits[row] = v;
+                    if (argmax_precedes(v, row, best_v, best_i)) {
+                        best_v = v;
+                        best_i = row;
+                    }
+                }
+            }
+            if (row0 + kLmPrefetch < row1)
+                lm_rows(args.lm_head, x, row0 + kLmPrefetch, row1, lane, LogitsPlainOut{args.logits}, best_v,
+                        best_i);
             wg_argmax(best_v, best_i, red_v, red_i);
-            // Release this token's K/V cache rows (every wave) before signalling the argmax.
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            FLUX_TRACE_POINT(2);
+            // This token's K/V cache rows were written through (agent-scope stores); wait
+            // until every wave's stores are acknowledged before signalling the argmax.  The
+            // rows are read by later tokens only, from lines no CU has cached yet.
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (threadIdx.x == 0) {
+            if (tid_opaque() == 0) {
                 ll_store(ll_arg + 2 * wg, best_v, ep_arg);
                 ll_store(ll_arg + 2 * wg + 1, __int_as_float(static_cast<int>(best_i)), ep_arg);
             }
             // Every workgroup reduces all G partials (thread t < G reads partial t).
             float v = -INFINITY;
             int64_t i = INT64_MAX;
-            if (threadIdx.x < G) {
-                const int idx[2] = {2 * static_cast<int>(threadIdx.x), 2 * static_cast<int>(threadIdx.x) + 1};
+            if (static_cast<int>(tid_opaque()) < G) {
+                const int idx[2] = {2 * static_cast<int>(tid_opaque()), 2 * static_cast<int>(tid_opaque()) + 1};
                 float pv[2];
                 LLIn{ll_arg, ep_arg, wctx}.fetch(idx, pv);
                 v = pv[0];
                 i = static_cast<int64_t>(__float_as_int(pv[1]));
             }
-            // wave-level then workgroup-level argmax
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) {
                 const float ov = __shfl_xor(v, off, kWave);
@@ -704,11 +976,11 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 }
             }
             wg_argmax(v, i, red_v, red_i);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            if (threadIdx.x == 0) token_shared = (i >= 0 && i < args.vocab) ? i : 0;
+            FLUX_TRACE_POINT(3);
+            if (tid_opaque() == 0) token_shared = (i >= 0 && i < args.vocab) ? i : 0;
             __syncthreads();
             const int64_t next = token_shared;
-            if (wg == 0 && threadIdx.x == 0) {
+            if (wg == 0 && tid_opaque() == 0) {
                 *args.input_token = next;
                 if (step >= 0 && step < args.generated_capacity) args.generated[step] = next;
                 *args.generation_step = step + 1;
@@ -721,7 +993,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         }
     }
     __syncthreads();
-    if (wg == 0 && threadIdx.x == 0) *args.token_counter = counter0 + static_cast<uint32_t>(args.steps);
+    if (wg == 0 && tid_opaque() == 0) *args.token_counter = counter0 + static_cast<uint32_t>(args.steps);
 }
 
 // ---------------------------------------------------------------------------
@@ -732,8 +1004,8 @@ __global__ void __launch_bounds__(kThreads) qkv_rope_cache_kernel(const float* h
                                                                   const float* sin_table, const int64_t* position_ptr,
                                                                   int64_t capacity, float* key_cache, float* value_cache,
                                                                   float* q_out) {
-    const int lane = threadIdx.x & 63;
-    const int gw = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int lane = tid_opaque() & 63;
+    const int gw = (tid_opaque() >> 6) * gridDim.x + blockIdx.x;
     const int TW = gridDim.x * kWavesPerWG;
     const int64_t position = *position_ptr;
     if (position < 0 || position >= capacity) return;
@@ -764,7 +1036,7 @@ __global__ void __launch_bounds__(kThreads) attn_partial_kernel(const float* q_p
     // Every position including the current one is read from the cache here.
     AttnChunk ch;
     attn_prefetch(key_cache + g * capacity * kHeadDim, value_cache + g * capacity * kHeadDim, begin, end, attended, ch);
-    const int quad = threadIdx.x & 15;
+    const int quad = tid_opaque() & 15;
     float4 q4[kGroup];
 #pragma unroll
     for (int h = 0; h < kGroup; ++h)
@@ -786,8 +1058,8 @@ __global__ void __launch_bounds__(kThreads) attn_merge_kernel(const float* parti
 
 __global__ void __launch_bounds__(kThreads) linear576_residual_kernel(const float* x, const float* w, const float* residual,
                                                                       float* out, int rows) {
-    const int lane = threadIdx.x & 63;
-    const int gw = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int lane = tid_opaque() & 63;
+    const int gw = (tid_opaque() >> 6) * gridDim.x + blockIdx.x;
     const int TW = gridDim.x * kWavesPerWG;
     for (int row = gw; row < rows; row += TW) {
         float wr[9], a[9];
@@ -800,8 +1072,8 @@ __global__ void __launch_bounds__(kThreads) linear576_residual_kernel(const floa
 
 __global__ void __launch_bounds__(kThreads) gate_up_swiglu_kernel(const float* hidden, const float* norm_w, float eps,
                                                                   const float* gate_up, float* out) {
-    const int lane = threadIdx.x & 63;
-    const int gw = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int lane = tid_opaque() & 63;
+    const int gw = (tid_opaque() >> 6) * gridDim.x + blockIdx.x;
     const int TW = gridDim.x * kWavesPerWG;
     for (int j = gw; j < kInter; j += TW) {
         float wg_[9], wu[9], r[9], x[9];
@@ -822,8 +1094,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_swiglu_kernel(const float* h
 
 __global__ void __launch_bounds__(kThreads) down_residual_kernel(const float* s, const float* w, const float* residual,
                                                                  float* out) {
-    const int lane = threadIdx.x & 63;
-    const int gw = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int lane = tid_opaque() & 63;
+    const int gw = (tid_opaque() >> 6) * gridDim.x + blockIdx.x;
     const int TW = gridDim.x * kWavesPerWG;
     for (int row = gw; row < kHidden; row += TW) {
         float wr[24], sv[24];
@@ -843,8 +1115,8 @@ __global__ void __launch_bounds__(kThreads) lm_head_partial_kernel(const float* 
                                                                    float* part_v, int64_t* part_i) {
     __shared__ float red_v[kWavesPerWG];
     __shared__ int64_t red_i[kWavesPerWG];
-    const int lane = threadIdx.x & 63;
-    const int gw = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    const int lane = tid_opaque() & 63;
+    const int gw = (tid_opaque() >> 6) * gridDim.x + blockIdx.x;
     const int TW = gridDim.x * kWavesPerWG;
     const int64_t per = (vocab + TW - 1) / TW;
     const int64_t row0 = per * gw < vocab ? per * gw : vocab;
@@ -861,7 +1133,7 @@ __global__ void __launch_bounds__(kThreads) lm_head_partial_kernel(const float* 
     int64_t best_i = INT64_MAX;
     lm_rows(lm_head, x, row0, row1, lane, LogitsPlainOut{logits}, best_v, best_i);
     wg_argmax(best_v, best_i, red_v, red_i);
-    if (threadIdx.x == 0) {
+    if (tid_opaque() == 0) {
         part_v[blockIdx.x] = best_v;
         part_i[blockIdx.x] = best_i;
     }
@@ -877,7 +1149,7 @@ __global__ void __launch_bounds__(kThreads) argmax_finish_kernel(const float* pa
     __shared__ int64_t red_i[kWavesPerWG];
     float v = -INFINITY;
     int64_t i = INT64_MAX;
-    for (int64_t k = threadIdx.x; k < n; k += kThreads) {
+    for (int64_t k = tid_opaque(); k < n; k += kThreads) {
         const float cv = part_v[k];
         const int64_t ci = part_i ? part_i[k] : k;
         if (argmax_precedes(cv, ci, v, i)) {
@@ -895,7 +1167,7 @@ __global__ void __launch_bounds__(kThreads) argmax_finish_kernel(const float* pa
         }
     }
     wg_argmax(v, i, red_v, red_i);
-    if (threadIdx.x == 0) {
+    if (tid_opaque() == 0) {
         const int64_t selected = i == INT64_MAX ? 0 : i;
         *token = selected;
         if (step != nullptr) {
@@ -913,7 +1185,7 @@ __global__ void __launch_bounds__(kThreads) argmax_finish_kernel(const float* pa
 __global__ void install_state_kernel(const int64_t* token_src, int64_t position_value, int64_t step_value,
                                      int write_generated0, int64_t* input_token, int64_t* position,
                                      int64_t* cache_length, int64_t* step, int64_t* generated) {
-    if (threadIdx.x != 0) return;
+    if (tid_opaque() != 0) return;
     const int64_t token = *token_src;
     *input_token = token;
     *position = position_value;
@@ -927,14 +1199,14 @@ __global__ void rmsnorm_rows_kernel(const float* x, const float* w, float* out, 
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
         const float* xr = x + row * cols;
         float ss = 0.0f;
-        for (int c = threadIdx.x; c < cols; c += blockDim.x) ss = fmaf(xr[c], xr[c], ss);
+        for (int c = tid_opaque(); c < cols; c += blockDim.x) ss = fmaf(xr[c], xr[c], ss);
         ss = wave_sum(ss);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        if ((tid_opaque() & 63) == 0) red[tid_opaque() >> 6] = ss;
         __syncthreads();
         float total = 0.0f;
         for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += red[w];
         const float inv = rms_inverse(total, cols, eps);
-        for (int c = threadIdx.x; c < cols; c += blockDim.x) out[row * cols + c] = w[c] * (xr[c] * inv);
+        for (int c = tid_opaque(); c < cols; c += blockDim.x) out[row * cols + c] = w[c] * (xr[c] * inv);
         __syncthreads();
     }
 }
@@ -944,18 +1216,18 @@ __global__ void residual_rmsnorm_rows_kernel(const float* hidden, const float* r
     __shared__ float red[kWavesPerWG];
     for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
         float ss = 0.0f;
-        for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+        for (int c = tid_opaque(); c < cols; c += blockDim.x) {
             const float r = hidden[row * cols + c] + residual[row * cols + c];
             residual_out[row * cols + c] = r;
             ss = fmaf(r, r, ss);
         }
         ss = wave_sum(ss);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        if ((tid_opaque() & 63) == 0) red[tid_opaque() >> 6] = ss;
         __syncthreads();
         float total = 0.0f;
         for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += red[w];
         const float inv = rms_inverse(total, cols, eps);
-        for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+        for (int c = tid_opaque(); c < cols; c += blockDim.x) {
             const float r = hidden[row * cols + c] + residual[row * cols + c];
             norm_out[row * cols + c] = w[c] * (r * inv);
         }
@@ -969,8 +1241,20 @@ __global__ void residual_rmsnorm_rows_kernel(const float* hidden, const float* r
 // Host launchers.
 
 size_t ll_arena_words() { return LLLayout::kTotal; }
+
+#ifdef FLUX_TRACE
+extern "C" int flux_debug_trace(uint64_t* host_out) {
+    return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_trace), sizeof(g_flux_trace)));
+}
+extern "C" int flux_debug_trace_all(uint64_t* host_out) {
+    return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_trace_all), sizeof(g_flux_trace_all)));
+}
+#endif
 int fused_decode_threads() { return kThreads; }
-size_t fused_decode_dynamic_lds() { return 96 * 1024; }
+size_t fused_decode_dynamic_lds() {
+    // K/V staging of one attention chunk (also keeps one workgroup per CU).
+    return 2 * kAttnMaxIter * kPosSlots * kHeadDim * sizeof(float);
+}
 
 int max_attention_positions(int grid) {
     const int chunks = grid / kKVHeads < kMaxAttnChunks ? grid / kKVHeads : kMaxAttnChunks;

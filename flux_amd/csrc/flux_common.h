@@ -43,23 +43,52 @@ struct LayerWeights {
 // Wave64 helpers.  Butterfly (xor) reductions leave the identical value in every
 // lane because IEEE addition/max are commutative, so no broadcast is needed and
 // results are bitwise deterministic.
+// DPP lane moves inside a row of 16 lanes (VALU speed, no LDS crossbar).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppRowRor8 = 0x128;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+
+// Sum over each row of 16 lanes; every lane of the row ends with the same value
+// (each step adds a commutative pair).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_move<kDppRowRor8>(v);
+    v += dpp_move<kDppRowRor4>(v);
+    v += dpp_move<kDppQuadXor2>(v);
+    v += dpp_move<kDppQuadXor1>(v);
+    return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_move<kDppRowRor8>(v));
+    v = fmaxf(v, dpp_move<kDppRowRor4>(v));
+    v = fmaxf(v, dpp_move<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_move<kDppQuadXor1>(v));
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    v = row16_max(v);
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    v = fmaxf(v, __shfl_xor(v, 32, kWave));
     return v;
 }
 
 template <int kWidth>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = kWidth / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    static_assert(kWidth == 16, "only 16-lane groups are used");
+    return row16_sum(v);
 }
 
 // Lane slicing of a 576-vector: lane owns [4l,4l+4) , [256+4l, 256+4l+4) and 512+l.
@@ -102,6 +131,12 @@ __device__ __forceinline__ float rms_inverse(float sum_squares, int width, float
     const float mean = sum_squares / static_cast<float>(width);
     return 1.0f / sqrtf(mean + eps);
 }
+
+// Softmax exponentials are evaluated in the log2 domain with the hardware
+// v_exp_f32 (2^x): scores are pre-multiplied by log2(e), so exp(s - m) is
+// exp2(s*log2e - m*log2e).  Relative error stays at the 1e-6 level.
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // SiLU as torch's CPU kernel rounds it: x / (1 + exp(-x)).
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }

@@ -213,6 +213,7 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
+    const float scale2 = scale * kLog2e;  // scores in log2 units
     const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
     const int64_t k_tiles = last_key / kKTile + 1;
     for (int64_t kt = 0; kt < k_tiles; ++kt) {
@@ -253,7 +254,7 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t key = k0 + 16 * kb + 4 * (lane >> 4) + r;
-                const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale : -INFINITY;
+                const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale2 : -INFINITY;
                 s_acc[kb][r] = v;
                 tile_max = fmaxf(tile_max, v);
             }
@@ -261,13 +262,13 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
         const float m_new = fmaxf(m_run, tile_max);
-        const float alpha = m_new == -INFINITY ? 1.0f : (m_run == -INFINITY ? 0.0f : expf(m_run - m_new));
+        const float alpha = m_new == -INFINITY ? 1.0f : (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - m_new));
         float psum = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = s_acc[kb][r] == -INFINITY ? 0.0f : expf(s_acc[kb][r] - m_new);
+                const float p = s_acc[kb][r] == -INFINITY ? 0.0f : fast_exp2(s_acc[kb][r] - m_new);
                 s_acc[kb][r] = p;
                 psum += p;
             }

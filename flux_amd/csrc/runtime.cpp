@@ -45,8 +45,13 @@ int decode_grid() {
     int blocks = 0;
     check_hip(fused_decode_occupancy(&blocks), "querying fused decode occupancy");
     if (blocks < 1) throw FluxError(FLUX_ERROR_HIP, "flux native decode: fused decode kernel cannot be resident");
-    // One workgroup per CU; every workgroup must be co-resident (they exchange data).
-    return std::min(cus, 3 * kMaxAttnChunks);
+    // One workgroup per CU; every workgroup must be co-resident (they exchange data),
+    // and the fused kernel maps one work unit per wave, which needs 8 * grid >= 1536.
+    const int grid = std::min(cus, 3 * kMaxAttnChunks);
+    if (grid < 192)
+        throw FluxError(FLUX_ERROR_HIP, "flux native decode: the fused decode kernel needs at least 192 CUs, found " +
+                                            std::to_string(cus));
+    return grid;
 }
 
 }  // namespace
