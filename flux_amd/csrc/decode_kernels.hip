@@ -47,8 +47,7 @@ __device__ __forceinline__ unsigned tid_opaque() {
 
 constexpr int kThreads = 512;
 constexpr int kWavesPerWG = kThreads / kWave;
-constexpr int kPosSlots = kThreads / 16;  // attention: 16 lanes (4 dims each) per position
-constexpr int kAttnMaxIter = 7;           // positions per WG <= kPosSlots * kAttnMaxIter = 224
+constexpr int kAttnRows = 224;            // attention rows per workgroup (LDS-resident K/V)
 constexpr int kLmBatch = 8;
 constexpr uint64_t kTimeoutTicks = 20ull * 1000 * 1000;  // 200 ms of the 100 MHz wall clock
 
@@ -290,180 +289,209 @@ __device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float 
 }
 
 // ---------------------------------------------------------------------------
-// Phase B: attention partial for (KV group g, chunk c) over positions
-// [begin, end).  Positions < `current` come from the cache (prefetched before the
-// query is available); position `current` (if inside) comes from the new K/V.
-// Thread t: position slot t/16, dims 4*(t%16)..+3.  Output per query head:
-// o[64] (unnormalised), m, l.
-struct AttnChunk {
-    float4 k[kAttnMaxIter];
-    float4 v[kAttnMaxIter];
-    __device__ __forceinline__ float4 key(int i, int64_t, int) const { return k[i]; }
-    __device__ __forceinline__ float4 value(int i, int64_t, int) const { return v[i]; }
-};
+// Phase B: attention partial for (KV group g, chunk c) over the chunk's rows
+// [begin, end), all resident in LDS when the compute starts.
+//
+// LDS layout of a chunk (row r = position - begin, kAttnRows rows at most):
+//   K: the 16-byte piece c (dims 4c..4c+3) of row r sits at r*64 + 4*(c ^ (r & 15)).
+//      QK reads one piece of 64 different rows per instruction; the xor spreads
+//      those reads over all banks.
+//   V: natural order, r*64 + d; PV reads one row per instruction, lane = dim.
+// Cached rows are copied HBM -> LDS with global_load_lds_dwordx4 (no register
+// staging); the current row comes from the QKV phase.
+//
+// Compute (3 query heads share the chunk):
+//   QK  thread (position p = t & 127 [+128], part = t >> 7): dims 16*part..+15
+//       of all 3 heads -> partial scores in LDS `sp`.
+//   max waves 0..5 = (head, half of the positions): sum the 4 parts, scale, max
+//       over the half (one wave reduction), p = 2^(s - m_half) -> LDS `pl`,
+//       l_half.
+//   PV  wave w (positions 16w..16w+15 [+128], all in half w >> 2), lane = dim.
+//   combine  threads (head, dim): rescale the two halves to the chunk maximum.
+// Output per query head: o[64] (unnormalised), m, l.
+constexpr int kAttnScoreStride = 256;                // sp/pl row stride (positions)
 
-// LDS-staged rows of the fused kernel (row r = pos - begin).
-struct AttnLdsRows {
-    const float* k_lds;
-    const float* v_lds;
-    int64_t begin;
-    __device__ __forceinline__ float4 key(int, int64_t pos, int quad) const {
-        return *reinterpret_cast<const float4*>(k_lds + (pos - begin) * kHeadDim + 4 * quad);
-    }
-    __device__ __forceinline__ float4 value(int, int64_t pos, int quad) const {
-        return *reinterpret_cast<const float4*>(v_lds + (pos - begin) * kHeadDim + 4 * quad);
-    }
-};
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__device__ __forceinline__ void attn_prefetch(const float* __restrict__ key_cache_g, const float* __restrict__ value_cache_g,
-                                              int64_t begin, int64_t end, int64_t current, AttnChunk& ch) {
-    const int slot = tid_opaque() >> 4;
-    const int quad = tid_opaque() & 15;
-#pragma unroll
-    for (int i = 0; i < kAttnMaxIter; ++i) {
-        const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
-        if (pos < end && pos < current) {
-            ch.k[i] = *reinterpret_cast<const float4*>(key_cache_g + pos * kHeadDim + 4 * quad);
-            ch.v[i] = *reinterpret_cast<const float4*>(value_cache_g + pos * kHeadDim + 4 * quad);
-        } else {
-            ch.k[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            ch.v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-}
+__device__ __forceinline__ int attn_k_index(int r, int d) { return r * kHeadDim + 4 * ((d >> 2) ^ (r & 15)) + (d & 3); }
 
-// Fused-kernel variant: stage the chunk's cached K/V rows [begin, begin + rows)
-// straight into LDS with global_load_lds_dwordx4 (no register staging).  Each
-// instruction moves 1 KB = 4 rows; wave w moves blocks w, w+8, ...
-__device__ __forceinline__ void attn_stage_lds(const float* __restrict__ key_cache_g,
-                                               const float* __restrict__ value_cache_g, int64_t begin, int rows,
-                                               float* k_lds, float* v_lds) {
+// Copy rows [begin, begin + rows) of one KV head into the chunk's LDS layout.
+// One instruction moves 4 rows (1 KB): lane l -> row 4b + l/16, slot l%16.
+// Waves [first_wave, kWavesPerWG) issue the copies.
+__device__ __forceinline__ void attn_stage_lds(const float* __restrict__ key_g, const float* __restrict__ value_g,
+                                               int64_t begin, int rows, float* k_lds, float* v_lds,
+                                               int first_wave) {
     const int lane = tid_opaque() & 63;
-    const int wave = tid_opaque() >> 6;
+    const int wave = wave_uniform(static_cast<int>(tid_opaque() >> 6));
     const int blocks = (rows + 3) >> 2;
-    for (int b = wave; b < blocks; b += kWavesPerWG) {
-        if (4 * b + (lane >> 4) < rows) {
-            const int64_t offset = (begin + 4 * b) * kHeadDim + 4 * lane;
-            __builtin_amdgcn_global_load_lds(key_cache_g + offset, k_lds + b * 256, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(value_cache_g + offset, v_lds + b * 256, 16, 0, 0);
+    const int nwaves = kWavesPerWG - first_wave;
+    const int r_in = lane >> 4;
+    const int slot = lane & 15;
+    for (int b = wave - first_wave; b < blocks && b >= 0; b += nwaves) {
+        const int r = 4 * b + r_in;
+        if (r < rows) {
+            const int64_t row = (begin + r) * kHeadDim;
+            __builtin_amdgcn_global_load_lds(key_g + row + 4 * (slot ^ (r & 15)), k_lds + b * 256, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(value_g + row + 4 * slot, v_lds + b * 256, 16, 0, 0);
         }
     }
 }
 
-// q4[h] = query dims of this thread for the 3 heads; knew/vnew = dims of the new row.
-// red: LDS scratch of kWavesPerWG * kGroup * 66 floats.
-template <class Rows, class POut>
-__device__ __forceinline__ void attn_compute(Rows& ch, const float4 (&q4)[kGroup], float4 knew, float4 vnew,
-                                             int64_t begin, int64_t end, int64_t current, float scale,
-                                             float* red, const POut& out) {
-    const int slot = tid_opaque() >> 4;
-    const int quad = tid_opaque() & 15;
-    const int lane = tid_opaque() & 63;
-    const int wave = tid_opaque() >> 6;
-    float s[kGroup][kAttnMaxIter];
-    float m[kGroup];
+// Scratch LDS of attn_compute: sp [4][kGroup][256] partial scores, pl [256][4]
+// probabilities, red [8][kGroup][64] per-wave outputs + 12 (m, l) words.
+struct AttnScratch {
+    float* sp;
+    float* pl;
+    float* red;
+};
+constexpr int kAttnSpFloats = 4 * kGroup * kAttnScoreStride;
+constexpr int kAttnPlFloats = 4 * kAttnScoreStride;
+constexpr int kAttnRedFloats = kWavesPerWG * kGroup * kHeadDim + 4 * kGroup;
+
+// qv: the 3 query rows (LDS, 192 floats).  rows <= kAttnRows.  scale2 = scale*log2(e).
+template <class POut>
+__device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_lds, const float* qv, int rows,
+                                             float scale2, const AttnScratch& ws, const POut& out) {
+    const int t = tid_opaque();
+    const int lane = t & 63;
+    const int wave = wave_uniform(t >> 6);
+    const int passes = rows > 128 ? 2 : 1;
+    // ---- QK: partial dot products over 16 dims ----
+    {
+        const int part = wave >> 1;
+        float q[kGroup][16];
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h) m[h] = -INFINITY;
-    const int iters = static_cast<int>((end - begin + kPosSlots - 1) / kPosSlots);
-    const float scale2 = scale * kLog2e;  // scores in log2 units
+        for (int h = 0; h < kGroup; ++h)
 #pragma unroll
-    for (int i = 0; i < kAttnMaxIter; ++i) {
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = *reinterpret_cast<const float4*>(qv + h * kHeadDim + 16 * part + 4 * k);
+                q[h][4 * k] = a.x;
+                q[h][4 * k + 1] = a.y;
+                q[h][4 * k + 2] = a.z;
+                q[h][4 * k + 3] = a.w;
+            }
+        for (int ps = 0; ps < passes; ++ps) {
+            const int p = ps * 128 + (wave & 1) * 64 + lane;
+            const int pr = p < rows ? p : 0;
+            const int sw = pr & 15;
+            const float* krow = k_lds + pr * kHeadDim;
+            float4 kk[4];
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) s[h][i] = -INFINITY;
-        if (i >= iters) continue;
-        const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
-        const bool valid = pos < end;
-        const float4 kr = pos == current ? knew : ch.key(i, pos, quad);
+            for (int k = 0; k < 4; ++k) kk[k] = *reinterpret_cast<const float4*>(krow + 4 * ((4 * part + k) ^ sw));
+            float acc[kGroup] = {0.f, 0.f, 0.f};
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            float part = q4[h].x * kr.x;
-            part = fmaf(q4[h].y, kr.y, part);
-            part = fmaf(q4[h].z, kr.z, part);
-            part = fmaf(q4[h].w, kr.w, part);
-            const float dot = group_sum<16>(part);
-            s[h][i] = valid ? dot * scale2 : -INFINITY;
-            m[h] = fmaxf(m[h], s[h][i]);
-        }
-    }
-    // Max over the 4 slots of this wave, then over waves.
+            for (int k = 0; k < 4; ++k) {
 #pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        m[h] = fmaxf(m[h], __shfl_xor(m[h], 16, kWave));
-        m[h] = fmaxf(m[h], __shfl_xor(m[h], 32, kWave));
-    }
-    float* red_m = red;                                // [waves][kGroup]
-    float* red_l = red + kWavesPerWG * kGroup;         // [waves][kGroup]
-    float* red_o = red + 2 * kWavesPerWG * kGroup;     // [waves][kGroup][64]
-    if (lane == 0) {
+                for (int h = 0; h < kGroup; ++h) {
+                    acc[h] = fmaf(q[h][4 * k], kk[k].x, acc[h]);
+                    acc[h] = fmaf(q[h][4 * k + 1], kk[k].y, acc[h]);
+                    acc[h] = fmaf(q[h][4 * k + 2], kk[k].z, acc[h]);
+                    acc[h] = fmaf(q[h][4 * k + 3], kk[k].w, acc[h]);
+                }
+            }
+            float* dst = ws.sp + part * (kGroup * kAttnScoreStride) + p;
 #pragma unroll
-        for (int h = 0; h < kGroup; ++h) red_m[wave * kGroup + h] = m[h];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        float mm = red_m[h];
-        for (int w = 1; w < kWavesPerWG; ++w) mm = fmaxf(mm, red_m[w * kGroup + h]);
-        m[h] = mm;
-    }
-    float l[kGroup];
-    float4 o[kGroup];
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-        l[h] = 0.0f;
-        o[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m[h] == -INFINITY) continue;
-#pragma unroll
-        for (int i = 0; i < kAttnMaxIter; ++i) {
-            if (s[h][i] == -INFINITY) continue;
-            const int64_t pos = begin + slot + static_cast<int64_t>(kPosSlots) * i;
-            const float4 vr = pos == current ? vnew : ch.value(i, pos, quad);
-            const float p = fast_exp2(s[h][i] - m[h]);
-            l[h] += p;
-            o[h].x = fmaf(p, vr.x, o[h].x);
-            o[h].y = fmaf(p, vr.y, o[h].y);
-            o[h].z = fmaf(p, vr.z, o[h].z);
-            o[h].w = fmaf(p, vr.w, o[h].w);
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h) {
-#pragma unroll
-        for (int off = 16; off <= 32; off <<= 1) {
-            l[h] += __shfl_xor(l[h], off, kWave);
-            o[h].x += __shfl_xor(o[h].x, off, kWave);
-            o[h].y += __shfl_xor(o[h].y, off, kWave);
-            o[h].z += __shfl_xor(o[h].z, off, kWave);
-            o[h].w += __shfl_xor(o[h].w, off, kWave);
-        }
-    }
-    if (lane < 16) {
-#pragma unroll
-        for (int h = 0; h < kGroup; ++h) {
-            float* dst = red_o + (wave * kGroup + h) * kHeadDim + 4 * quad;
-            dst[0] = o[h].x; dst[1] = o[h].y; dst[2] = o[h].z; dst[3] = o[h].w;
-            if (lane == 0) red_l[wave * kGroup + h] = l[h];
+            for (int h = 0; h < kGroup; ++h) dst[h * kAttnScoreStride] = acc[h];
         }
     }
     __syncthreads();
-    // Threads 0..191 finish (head h = t/64, dim d = t%64); thread t%64==0 also m,l.
-    if (tid_opaque() < kGroup * kHeadDim) {
-        const int h = tid_opaque() >> 6;
-        const int dim = tid_opaque() & 63;
-        float acc = 0.0f;
-        float lsum = 0.0f;
-        for (int w = 0; w < kWavesPerWG; ++w) {
-            acc += red_o[(w * kGroup + h) * kHeadDim + dim];
-            lsum += red_l[w * kGroup + h];
+    // ---- scores, per-half maximum, probabilities ----
+    float* red_ml = ws.red + kWavesPerWG * kGroup * kHeadDim;  // m[kGroup][2], l[kGroup][2]
+    if (wave < 2 * kGroup) {
+        const int h = wave >> 1;
+        const int half = wave & 1;
+        float s[2];
+        float m = -INFINITY;
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+            s[ps] = -INFINITY;
+            if (ps < passes) {
+                const int p = ps * 128 + half * 64 + lane;
+                const float* src = ws.sp + h * kAttnScoreStride + p;
+                const float v = (src[0] + src[kGroup * kAttnScoreStride]) +
+                                (src[2 * kGroup * kAttnScoreStride] + src[3 * kGroup * kAttnScoreStride]);
+                s[ps] = p < rows ? v * scale2 : -INFINITY;
+                m = fmaxf(m, s[ps]);
+            }
         }
-        out.put(h, dim, acc);
-        if (dim == 0) {
-            out.put(h, kHeadDim, m[h]);
-            out.put(h, kHeadDim + 1, lsum);
+        m = wave_max_uniform(m);
+        float l = 0.0f;
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+            if (ps < passes) {
+                const int p = ps * 128 + half * 64 + lane;
+                const float e = s[ps] == -INFINITY ? 0.0f : fast_exp2(s[ps] - m);
+                ws.pl[p * 4 + h] = e;
+                l += e;
+            }
+        }
+        l = wave_sum_uniform(l);
+        if (lane == 0) {
+            red_ml[h * 2 + half] = m;
+            red_ml[2 * kGroup + h * 2 + half] = l;
+        }
+    }
+    __syncthreads();
+    // ---- PV: lane = dim over this wave's 16 positions ----
+    {
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f;
+        for (int ps = 0; ps < passes; ++ps) {
+            const int base = ps * 128 + wave * 16;
+            if (base >= rows) break;
+            const float* vsrc = v_lds + base * kHeadDim + lane;
+            const float4* psrc = reinterpret_cast<const float4*>(ws.pl + base * 4);
+            if (base + 16 <= rows) {
+                float vv[16];
+                float4 pp[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    vv[j] = vsrc[j * kHeadDim];
+                    pp[j] = psrc[j];
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    o0 = fmaf(pp[j].x, vv[j], o0);
+                    o1 = fmaf(pp[j].y, vv[j], o1);
+                    o2 = fmaf(pp[j].z, vv[j], o2);
+                }
+            } else {
+                const int n = rows - base;
+                for (int j = 0; j < n; ++j) {
+                    const float v = vsrc[j * kHeadDim];
+                    const float4 pj = psrc[j];
+                    o0 = fmaf(pj.x, v, o0);
+                    o1 = fmaf(pj.y, v, o1);
+                    o2 = fmaf(pj.z, v, o2);
+                }
+            }
+        }
+        float* dst = ws.red + wave * (kGroup * kHeadDim) + lane;
+        dst[0] = o0;
+        dst[kHeadDim] = o1;
+        dst[2 * kHeadDim] = o2;
+    }
+    __syncthreads();
+    // ---- combine the 8 waves: halves rescaled to the chunk maximum ----
+    if (wave < kGroup) {
+        const int h = wave;
+        const float m0 = red_ml[h * 2], m1 = red_ml[h * 2 + 1];
+        const float M = fmaxf(m0, m1);
+        const float f0 = m0 == -INFINITY ? 0.0f : fast_exp2(m0 - M);
+        const float f1 = m1 == -INFINITY ? 0.0f : fast_exp2(m1 - M);
+        const float* src = ws.red + h * kHeadDim + lane;
+        constexpr int kS = kGroup * kHeadDim;
+        const float a0 = (src[0] + src[kS]) + (src[2 * kS] + src[3 * kS]);
+        const float a1 = (src[4 * kS] + src[5 * kS]) + (src[6 * kS] + src[7 * kS]);
+        out.put(h, lane, a0 * f0 + a1 * f1);
+        if (lane == 0) {
+            out.put(h, kHeadDim, M);
+            out.put(h, kHeadDim + 1, red_ml[2 * kGroup + h * 2] * f0 + red_ml[2 * kGroup + h * 2 + 1] * f1);
         }
     }
     __syncthreads();
 }
 
+// ---------------------------------------------------------------------------
 // Partial output addressing: partial (g, c) has kGroup * 66 slots.
 struct PartialPlainOut {
     float* p;
@@ -620,24 +648,34 @@ __device__ uint64_t g_flux_trace_all[512][16];
 
 // ---------------------------------------------------------------------------
 // Workgroup-cooperative LL fetch into LDS.  Word k (0 <= k < count) is read from
-// base + index(k); each thread polls at most kMax words in one batch.  Threads
-// with fewer words re-poll word index(0), which belongs to the same vector.
-template <int kMax, class IndexFn>
-__device__ __forceinline__ void wg_ll_fetch(const uint64_t* __restrict__ base, int count, IndexFn index,
-                                            uint32_t epoch, const WaitCtx& w, float* lds) {
+// base + index(k) and stored to *dest(k); threads [first_thread, kThreads) poll,
+// each at most kMax words in one batch.  Threads with fewer words poll nothing
+// extra (their slots re-read word index(0) but are not stored).
+template <int kMax, class IndexFn, class DestFn>
+__device__ __forceinline__ void wg_ll_fetch_to(const uint64_t* __restrict__ base, int count, IndexFn index,
+                                               DestFn dest, int first_thread, uint32_t epoch, const WaitCtx& w) {
+    const int me = static_cast<int>(tid_opaque()) - first_thread;
+    const int nthreads = kThreads - first_thread;
+    if (me < 0) return;
     int idx[kMax];
     float v[kMax];
 #pragma unroll
     for (int j = 0; j < kMax; ++j) {
-        const int k = static_cast<int>(tid_opaque()) + j * kThreads;
+        const int k = me + j * nthreads;
         idx[j] = index(k < count ? k : 0);
     }
-    if (static_cast<int>(tid_opaque()) < count) ll_fetch<kMax>(base, idx, epoch, w, v);
+    if (me < count) ll_fetch<kMax>(base, idx, epoch, w, v);
 #pragma unroll
     for (int j = 0; j < kMax; ++j) {
-        const int k = static_cast<int>(tid_opaque()) + j * kThreads;
-        if (k < count) lds[k] = v[j];
+        const int k = me + j * nthreads;
+        if (k < count) *dest(k) = v[j];
     }
+}
+
+template <int kMax, class IndexFn>
+__device__ __forceinline__ void wg_ll_fetch(const uint64_t* __restrict__ base, int count, IndexFn index,
+                                            uint32_t epoch, const WaitCtx& w, float* lds) {
+    wg_ll_fetch_to<kMax>(base, count, index, [=](int k) { return lds + k; }, 0, epoch, w);
 }
 
 struct Contiguous {
@@ -655,14 +693,16 @@ __device__ __forceinline__ void lds_slice576(const float* vec, int lane, float (
 // Requires gridDim.x * 8 >= 1536 (one unit per wave in every phase).
 __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs args) {
     __shared__ int abort_flag;
-    __shared__ float red[kWavesPerWG * kGroup * (kHeadDim + 2)];
+    __shared__ float red[kAttnRedFloats];
+    __shared__ __align__(16) float attn_sp[kAttnSpFloats];
+    __shared__ __align__(16) float attn_pl[kAttnPlFloats];
     __shared__ int64_t red_i[kWavesPerWG];
     __shared__ float red_v[kWavesPerWG];
     __shared__ int64_t token_shared;
     __shared__ float hvec[kHidden];   // layer input h (residual of C)
     __shared__ float rvec[kHidden];   // post-attention residual r (residual of E)
-    __shared__ float vec[kInter];     // attention output / SwiGLU output / q,k,v of the group
-    extern __shared__ float part[];   // merge staging [chunks][66]; sized to keep one WG per CU
+    __shared__ __align__(16) float vec[kInter];  // attention output / SwiGLU output / q of the group
+    extern __shared__ __align__(16) float part[];  // K/V rows of the attention chunk; merge staging
 
     const int lane = tid_opaque() & 63;
     const int wave = tid_opaque() >> 6;
@@ -747,36 +787,36 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 const int64_t cached_end = end < position ? end : position;
                 const int cached_rows = cached_end > begin ? static_cast<int>(cached_end - begin) : 0;
                 float* k_lds = part;
-                float* v_lds = part + kAttnMaxIter * kPosSlots * kHeadDim;
+                float* v_lds = part + kAttnRows * kHeadDim;
+                // Waves 0-1 may still be finishing the QKV phase: waves 2-7 stage the cached
+                // rows and poll the query (and the current row) for the whole workgroup.
                 attn_stage_lds(key_layer + g * head_stride, value_layer + g * head_stride, begin, cached_rows, k_lds,
-                               v_lds);
+                               v_lds, 2);
                 const bool has_current = position >= begin && position < end;
-                // vec[0..191] = q of heads 3g..3g+2; vec[192..319] = new k row, new v row.
+                const int cur = static_cast<int>(position - begin);
+                // Words 0..191: q of heads 3g..3g+2 -> vec; 192..255: new k row; 256..319: new v row.
                 const int qbase = g * kGroup * kHeadDim;
                 const int kbase = kQHeads * kHeadDim + g * kHeadDim;
-                wg_ll_fetch<1>(ll + LLLayout::kQkv, has_current ? kGroup * kHeadDim + 2 * kHeadDim : kGroup * kHeadDim,
-                               [=](int k) {
-                                   return k < kGroup * kHeadDim ? qbase + k
-                                                                : kbase + ((k - kGroup * kHeadDim) >> 6) *
-                                                                              (kKVHeads * kHeadDim) +
-                                                                      ((k - kGroup * kHeadDim) & 63);
-                               },
-                               ep, wctx, vec);
+                wg_ll_fetch_to<1>(
+                    ll + LLLayout::kQkv, has_current ? kGroup * kHeadDim + 2 * kHeadDim : kGroup * kHeadDim,
+                    [=](int k) {
+                        return k < kGroup * kHeadDim
+                                   ? qbase + k
+                                   : kbase + ((k - kGroup * kHeadDim) >> 6) * (kKVHeads * kHeadDim) +
+                                         ((k - kGroup * kHeadDim) & 63);
+                    },
+                    [=](int k) {
+                        if (k < kGroup * kHeadDim) return vec + k;
+                        const int d = (k - kGroup * kHeadDim) & 63;
+                        return k < kGroup * kHeadDim + kHeadDim ? k_lds + attn_k_index(cur, d)
+                                                                : v_lds + cur * kHeadDim + d;
+                    },
+                    2 * kWave, ep, wctx);
                 __builtin_amdgcn_s_waitcnt(0);  // LDS-direct K/V loads have landed
                 __syncthreads();
                 FLUX_TRACE_POINT(3);
-                AttnLdsRows ch{k_lds, v_lds, begin};
-                const int quad = tid_opaque() & 15;
-                float4 q4[kGroup];
-#pragma unroll
-                for (int h = 0; h < kGroup; ++h)
-                    q4[h] = *reinterpret_cast<const float4*>(vec + h * kHeadDim + 4 * quad);
-                float4 knew = make_float4(0.f, 0.f, 0.f, 0.f), vnew = knew;
-                if (has_current) {
-                    knew = *reinterpret_cast<const float4*>(vec + kGroup * kHeadDim + 4 * quad);
-                    vnew = *reinterpret_cast<const float4*>(vec + kGroup * kHeadDim + kHeadDim + 4 * quad);
-                }
-                attn_compute(ch, q4, knew, vnew, begin, end, position, Lw.scale, red,
+                attn_compute(k_lds, v_lds, vec, static_cast<int>(end - begin), Lw.scale * kLog2e,
+                             AttnScratch{attn_sp, attn_pl, red},
                              PartialLLOut{ll + LLLayout::kPartials + (g * chunks + c) * partial_stride, ep});
             }
 
@@ -1025,7 +1065,11 @@ __global__ void __launch_bounds__(kThreads) attn_partial_kernel(const float* q_p
                                                                 const float* value_cache, const int64_t* position_ptr,
                                                                 int64_t capacity, float scale, int chunks,
                                                                 float* partials) {
-    __shared__ float red[kWavesPerWG * kGroup * (kHeadDim + 2)];
+    __shared__ float red[kAttnRedFloats];
+    __shared__ __align__(16) float attn_sp[kAttnSpFloats];
+    __shared__ __align__(16) float attn_pl[kAttnPlFloats];
+    __shared__ __align__(16) float qv[kGroup * kHeadDim];
+    extern __shared__ __align__(16) float part[];
     const int g = blockIdx.x % kKVHeads;
     const int c = blockIdx.x / kKVHeads;
     const int64_t position = *position_ptr;
@@ -1033,16 +1077,17 @@ __global__ void __launch_bounds__(kThreads) attn_partial_kernel(const float* q_p
     const int64_t attended = position + 1;
     int64_t begin, end;
     chunk_range(attended, chunks, c, begin, end);
-    // Every position including the current one is read from the cache here.
-    AttnChunk ch;
-    attn_prefetch(key_cache + g * capacity * kHeadDim, value_cache + g * capacity * kHeadDim, begin, end, attended, ch);
-    const int quad = tid_opaque() & 15;
-    float4 q4[kGroup];
-#pragma unroll
-    for (int h = 0; h < kGroup; ++h)
-        q4[h] = *reinterpret_cast<const float4*>(q_packed + (g * kGroup + h) * kHeadDim + 4 * quad);
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
-    attn_compute(ch, q4, zero, zero, begin, end, /*current=*/-1, scale, red,
+    const int rows = static_cast<int>(end - begin);
+    if (rows > kAttnRows) return;  // the launcher sizes chunks so this cannot happen
+    // Every row including the current one is read from the cache here.
+    float* k_lds = part;
+    float* v_lds = part + kAttnRows * kHeadDim;
+    attn_stage_lds(key_cache + g * capacity * kHeadDim, value_cache + g * capacity * kHeadDim, begin, rows, k_lds,
+                   v_lds, 0);
+    for (int k = tid_opaque(); k < kGroup * kHeadDim; k += kThreads) qv[k] = q_packed[g * kGroup * kHeadDim + k];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    attn_compute(k_lds, v_lds, qv, rows, scale * kLog2e, AttnScratch{attn_sp, attn_pl, red},
                  PartialPlainOut{partials + (g * chunks + c) * kGroup * (kHeadDim + 2)});
 }
 
@@ -1253,12 +1298,12 @@ extern "C" int flux_debug_trace_all(uint64_t* host_out) {
 int fused_decode_threads() { return kThreads; }
 size_t fused_decode_dynamic_lds() {
     // K/V staging of one attention chunk (also keeps one workgroup per CU).
-    return 2 * kAttnMaxIter * kPosSlots * kHeadDim * sizeof(float);
+    return 2 * kAttnRows * kHeadDim * sizeof(float);
 }
 
 int max_attention_positions(int grid) {
     const int chunks = grid / kKVHeads < kMaxAttnChunks ? grid / kKVHeads : kMaxAttnChunks;
-    return chunks * kPosSlots * kAttnMaxIter;
+    return chunks * kAttnRows;
 }
 
 hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream) {
@@ -1287,15 +1332,19 @@ hipError_t launch_qkv_rope_cache(const float* hidden, const float* norm_w, float
 hipError_t launch_gqa_decode(const float* q, const float* key_cache, const float* value_cache, const int64_t* position,
                              int64_t capacity, float scale, int chunks, float* partials, float* out,
                              hipStream_t stream) {
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(kKVHeads * chunks), dim3(kThreads), 0, stream, q, key_cache,
-                       value_cache, position, capacity, scale, chunks, partials);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_partial_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(fused_decode_dynamic_lds()));
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(kKVHeads * chunks), dim3(kThreads), fused_decode_dynamic_lds(), stream,
+                       q, key_cache, value_cache, position, capacity, scale, chunks, partials);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(kQHeads), dim3(kThreads), 0, stream, partials, chunks, out);
     return hipGetLastError();
 }
 
-int gqa_decode_max_positions(int chunks) { return chunks * kPosSlots * kAttnMaxIter; }
+int gqa_decode_max_positions(int chunks) { return chunks * kAttnRows; }
 
 hipError_t launch_linear576_residual(const float* x, const float* w, const float* residual, float* out, int rows,
                                      int grid, hipStream_t stream) {

@@ -85,6 +85,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Whole-wave reductions that end in a wave-uniform (scalar) value: row
+// reduction, then row_bcast15 / row_bcast31 fold rows 0..3 into lane 63, which
+// is read into an SGPR.  All VALU/DPP, no LDS crossbar.
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+    v = row16_sum(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowBcast15, 0xA, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowBcast31, 0xC, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max_uniform(float v) {
+    v = row16_max(v);
+    const int ninf = __float_as_int(-INFINITY);
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowBcast15, 0xA, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), kDppRowBcast31, 0xC, 0xF, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 template <int kWidth>
 __device__ __forceinline__ float group_sum(float v) {
     static_assert(kWidth == 16, "only 16-lane groups are used");
