@@ -250,16 +250,34 @@ __device__ __forceinline__ RopePair rope_pair(const float* __restrict__ cos_row,
     return RopePair{cos_row[d], sin_row[d], cos_row[d + 32], sin_row[d + 32]};
 }
 
+// Normalised QKV row pair of one unit.  The RMS scale multiplies the finished dot
+// products, q = inv_rms * sum_j (h_j * wn_j) * w_j, so the sum of squares and both
+// dot products reduce at the same time (one reduction latency instead of two);
+// the reductions end in wave-uniform values.  RoPE (products rounded separately,
+// packed_qkv_rope_cache_cuda.cu:40-48) and routing as the reference: q -> out[r],
+// k/v -> the cache row at the current position (and out[r]).  Lane 0 writes.
 template <class QOut>
-__device__ __forceinline__ void qkv_finish_rp(const QkvUnitWeights& w, const float (&x)[9], int unit, int lane,
-                                              const RopePair& rp, float* __restrict__ key_row_base,
-                                              float* __restrict__ value_row_base, int64_t head_stride,
-                                              const QOut& out) {
+__device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const float (&h)[9], const float (&wn)[9],
+                                                 float eps, int unit, int lane, const RopePair& rp,
+                                                 float* __restrict__ key_row_base, float* __restrict__ value_row_base,
+                                                 int64_t head_stride, const QOut& out) {
     int head, d, r0, r1;
     qkv_unit_rows(unit, head, d, r0, r1);
-    const float a = wave_sum(dot_lane<9>(x, w.w0));
-    const float b = wave_sum(dot_lane<9>(x, w.w1));
+    float ss = 0.0f, pa = 0.0f, pb = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+        ss = fmaf(h[j], h[j], ss);
+        const float hw = h[j] * wn[j];
+        pa = fmaf(hw, w.w0[j], pa);
+        pb = fmaf(hw, w.w1[j], pb);
+    }
+    ss = wave_sum_uniform(ss);
+    pa = wave_sum_uniform(pa);
+    pb = wave_sum_uniform(pb);
     if (lane != 0) return;
+    const float inv = rms_inverse(ss, kHidden, eps);
+    const float a = pa * inv;
+    const float b = pb * inv;
     float lo, hi;
     if (head < kQHeads + kKVHeads) {
         lo = rope_first(a, b, rp.c_lo, rp.s_lo);
@@ -278,14 +296,6 @@ __device__ __forceinline__ void qkv_finish_rp(const QkvUnitWeights& w, const flo
     }
     out.put(r0, lo);
     out.put(r1, hi);
-}
-
-template <class QOut>
-__device__ __forceinline__ void qkv_finish(const QkvUnitWeights& w, const float (&x)[9], int unit, int lane,
-                                           const float* __restrict__ cos_row, const float* __restrict__ sin_row,
-                                           float* __restrict__ key_row_base, float* __restrict__ value_row_base,
-                                           int64_t head_stride, const QOut& out) {
-    qkv_finish_rp(w, x, unit, lane, rope_pair(cos_row, sin_row, unit), key_row_base, value_row_base, head_stride, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -688,11 +698,35 @@ __device__ __forceinline__ void lds_slice576(const float* vec, int lane, float (
     for (int j = 0; j < 9; ++j) v[j] = vec[slice576_index(lane, j)];
 }
 
+// Layer descriptors are copied into LDS once per launch; a layer's descriptor is
+// read from there and moved into scalar registers (its pointers are wave-uniform),
+// so the weight loads of a phase need no memory round trip before they issue.
+__device__ __forceinline__ const float* uniform_ptr(const float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = static_cast<uint32_t>(wave_uniform(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint32_t hi = static_cast<uint32_t>(wave_uniform(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return reinterpret_cast<const float*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ LayerWeights uniform_desc(const LayerWeights& d) {
+    LayerWeights u;
+    u.input_norm = uniform_ptr(d.input_norm);
+    u.qkv = uniform_ptr(d.qkv);
+    u.o_proj = uniform_ptr(d.o_proj);
+    u.post_norm = uniform_ptr(d.post_norm);
+    u.gate_up = uniform_ptr(d.gate_up);
+    u.down = uniform_ptr(d.down);
+    u.eps = __int_as_float(wave_uniform(__float_as_int(d.eps)));
+    u.scale = __int_as_float(wave_uniform(__float_as_int(d.scale)));
+    return u;
+}
+
 // ---------------------------------------------------------------------------
 // The fused persistent decode kernel: `args.steps` greedy tokens per launch.
 // Requires gridDim.x * 8 >= 1536 (one unit per wave in every phase).
 __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs args) {
     __shared__ int abort_flag;
+    __shared__ LayerWeights layer_desc[kLayers];
     __shared__ float red[kAttnRedFloats];
     __shared__ __align__(16) float attn_sp[kAttnSpFloats];
     __shared__ __align__(16) float attn_pl[kAttnPlFloats];
@@ -716,6 +750,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     const int partial_stride = kGroup * (kHeadDim + 2);
 
     if (tid_opaque() == 0) abort_flag = 0;
+    if (tid_opaque() < kLayers) layer_desc[tid_opaque()] = args.layers[tid_opaque()];
     const uint32_t counter0 = *args.token_counter;
     int64_t token = *args.input_token;
     int64_t position = *args.position;
@@ -741,7 +776,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         const float* emb_row = args.embedding + (token_ok ? token : 0) * kHidden;
 
         for (int layer = 0; layer < kLayers; ++layer) {
-            const LayerWeights Lw = args.layers[layer];
+            const LayerWeights Lw = uniform_desc(layer_desc[layer]);
             const uint32_t ep = epoch_of(counter, layer);
             uint64_t* ll = args.ll + (layer & 1) * LLLayout::kParity;
             const uint64_t* ll_prev = args.ll + ((layer + 1) & 1) * LLLayout::kParity;
@@ -769,11 +804,10 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 __syncthreads();
                 FLUX_TRACE_POINT(1);
                 if (active) {
-                    float h[9], x[9];
+                    float h[9];
                     lds_slice576(hvec, lane, h);
-                    norm_slice_w(h, wn, Lw.eps, x);
-                    qkv_finish_rp(w, x, gw, lane, rp, key_layer + position * kHeadDim,
-                                  value_layer + position * kHeadDim, head_stride, LLOut{ll + LLLayout::kQkv, ep});
+                    qkv_unit_compute(w, h, wn, Lw.eps, gw, lane, rp, key_layer + position * kHeadDim,
+                                     value_layer + position * kHeadDim, head_stride, LLOut{ll + LLLayout::kQkv, ep});
                 }
             }
 
@@ -889,7 +923,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 if (active) {
                     float a[9];
                     lds_slice576(vec, lane, a);
-                    const float dot = wave_sum(dot_lane<9>(a, w));
+                    const float dot = wave_sum_uniform(dot_lane<9>(a, w));
                     if (lane == 0) ll_store(ll + LLLayout::kResid + gw, hvec[gw] + dot, ep);
                 }
                 __syncthreads();
@@ -909,12 +943,24 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 __syncthreads();
                 FLUX_TRACE_POINT(9);
                 if (active) {
-                    float r[9], x[9];
+                    // RMS scale applied after the dot products (see qkv_unit_compute).
+                    float r[9];
                     lds_slice576(rvec, lane, r);
-                    norm_slice_w(r, wn, Lw.eps, x);
-                    const float gsum = wave_sum(dot_lane<9>(x, wg_));
-                    const float usum = wave_sum(dot_lane<9>(x, wu));
-                    if (lane == 0) ll_store(ll + LLLayout::kSwiglu + gw, silu(gsum) * usum, ep);
+                    float ss = 0.0f, pg = 0.0f, pu = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 9; ++j) {
+                        ss = fmaf(r[j], r[j], ss);
+                        const float rw = r[j] * wn[j];
+                        pg = fmaf(rw, wg_[j], pg);
+                        pu = fmaf(rw, wu[j], pu);
+                    }
+                    ss = wave_sum_uniform(ss);
+                    pg = wave_sum_uniform(pg);
+                    pu = wave_sum_uniform(pu);
+                    if (lane == 0) {
+                        const float inv = rms_inverse(ss, kHidden, Lw.eps);
+                        ll_store(ll + LLLayout::kSwiglu + gw, silu(pg * inv) * (pu * inv), ep);
+                    }
                 }
                 __syncthreads();
                 FLUX_TRACE_POINT(12);
@@ -933,7 +979,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     float sv[24];
 #pragma unroll
                     for (int j = 0; j < 24; ++j) sv[j] = vec[slice1536_index(lane, j)];
-                    const float dot = wave_sum(dot_lane<24>(sv, w));
+                    const float dot = wave_sum_uniform(dot_lane<24>(sv, w));
                     if (lane == 0) ll_store(ll + LLLayout::kHidden + gw, rvec[gw] + dot, ep);
                 }
                 __syncthreads();
@@ -1052,12 +1098,13 @@ __global__ void __launch_bounds__(kThreads) qkv_rope_cache_kernel(const float* h
     for (int unit = gw; unit < kQKV / 2; unit += TW) {
         QkvUnitWeights w;
         qkv_load(qkv_w, unit, lane, w);
-        float h[9], x[9];
+        float h[9], wn[9];
         fetch_slice576(PlainIn{hidden}, lane, h);
-        norm_slice(h, norm_w, eps, lane, x);
-        qkv_finish(w, x, unit, lane, cos_table + position * kHeadDim, sin_table + position * kHeadDim,
-                   key_cache + position * kHeadDim, value_cache + position * kHeadDim, capacity * kHeadDim,
-                   PlainOut{q_out});
+        load_slice576(norm_w, lane, wn);
+        qkv_unit_compute(w, h, wn, eps, unit, lane,
+                         rope_pair(cos_table + position * kHeadDim, sin_table + position * kHeadDim, unit),
+                         key_cache + position * kHeadDim, value_cache + position * kHeadDim, capacity * kHeadDim,
+                         PlainOut{q_out});
     }
 }
 
