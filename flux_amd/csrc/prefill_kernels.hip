@@ -8,11 +8,12 @@
 // (online softmax with K/V tiles in shared memory, no score materialisation).
 //
 // MI355X design:
-//  * GEMM: 128x64 block tile, 4 waves stacked in M, each wave 32x64 computed with
-//    v_mfma_f32_32x32x2f32 (two 32x32 column tiles).  The epilogue consumes the
-//    accumulator layout directly: the two column tiles of a wave hold columns j
-//    and j+32 of the same rows, which is exactly the RoPE pair (QKV tile = one
-//    head) and the gate/up pair (gate/up tiles are interleaved 32+32).
+//  * GEMM: 128x128 (or 64x128) block tile, 4 waves in 2x2, each wave 64x64 (32x64)
+//    on v_mfma_f32_32x32x2f32; tiles stream HBM -> LDS with global_load_lds.  The
+//    epilogue consumes the accumulator layout directly: the two column tiles of a
+//    wave hold columns j and j+32 of the same rows, which is exactly the RoPE pair
+//    (a 64-column group = one head) and the gate/up pair (gate/up rows are
+//    interleaved 32+32 per group).
 //  * Attention: one block per (64-query tile, query head); 4 waves x 16 queries.
 //    S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x4f32, so the S^T
 //    accumulators are already the B operand of the PV product (no transpose).
@@ -29,11 +30,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 64;
+constexpr int kBN = 128;        // block tile columns: 2 waves x 64 (one epilogue column group each)
 constexpr int kBK = 16;
 constexpr int kGemmThreads = 256;
-constexpr int kAPad = 4;
 
 // MFMA 32x32x2 accumulator element r of lane l -> (row, col) inside the 32x32 tile.
 __device__ __forceinline__ int mfma32_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
@@ -55,7 +54,7 @@ __device__ __forceinline__ float rope_hi(float x, float paired, float c, float s
 template <GemmEpilogue E>
 __device__ __forceinline__ int b_row(int col, int n) {
     if constexpr (E == GemmEpilogue::kSwiglu) {
-        // Tile t (64 columns) = gate rows [32t, 32t+32) then up rows [half + 32t, ...).
+        // Column group t (64 columns) = gate rows [32t, 32t+32) then up rows [half + 32t, ...).
         const int half = n / 2;
         const int t = col >> 6;
         const int v = col & 63;
@@ -65,105 +64,157 @@ __device__ __forceinline__ int b_row(int col, int n) {
     }
 }
 
-template <GemmEpilogue E>
+// LDS tile layout (A: BM rows, B: 128 rows; 16 floats of K per row, 64 B): the
+// 16-byte piece c of row r sits at piece position c ^ ((r >> 2) & 3), so the 16
+// lanes of one ds_read_b128 pass (16 consecutive rows, same piece) cover all banks.
+__device__ __forceinline__ int tile_offset(int r, int c) { return r * kBK + 4 * (c ^ ((r >> 2) & 3)); }
+
+// One global_load_lds_dwordx4: each lane copies 16 B from `src` to lds + 16 * lane.
+__device__ __forceinline__ void lds_copy16(const float* src, float* lds) {
+    __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+
+// C = epilogue(A[M,K] * W[N,K]^T) on v_mfma_f32_32x32x2f32.  Block tile (64*MI) x 128,
+// 4 waves in 2 x 2, wave tile (32*MI) x 64.  K is consumed 16 at a time; MFMA
+// instruction s (0..7) of a stage pairs K index s (lanes 0-31) with s + 8 (lanes
+// 32-63), so each lane reads its 8 K values of a row with two ds_read_b128.
+// Tiles stream HBM -> LDS with global_load_lds (no register staging), double buffered.
+template <GemmEpilogue E, int MI>
 __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
-    __shared__ float a_s[2][kBK][kBM + kAPad];
-    __shared__ float b_s[2][kBK][kBN + kAPad];
+    constexpr int kBMt = 64 * MI;
+    __shared__ __align__(16) float a_s[2][kBMt * kBK];
+    __shared__ __align__(16) float b_s[2][kBN * kBK];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1;  // wave row
+    const int wn = wave & 1;   // wave column group (64 columns)
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBMt;
     const int n0 = blockIdx.x * kBN;
     const int K = args.k;
+    const bool group_valid = n0 + wn * 64 < args.n;
 
-    // Global -> LDS mapping: A tile 128x16 = 512 float4 (2 per thread), B 64x16 = 256 float4.
-    const int a_row = threadIdx.x >> 2;         // 0..63 (+64)
-    const int a_kq = (threadIdx.x & 3) * 4;     // 0,4,8,12
-    const int b_rowi = threadIdx.x >> 2;        // 0..63
-    const int64_t a_r0 = m0 + a_row;
-    const int64_t a_r1 = m0 + a_row + 64;
-    const float* a_p0 = args.a + (a_r0 < args.m ? a_r0 : 0) * K + a_kq;
-    const float* a_p1 = args.a + (a_r1 < args.m ? a_r1 : 0) * K + a_kq;
-    const bool a_ok0 = a_r0 < args.m;
-    const bool a_ok1 = a_r1 < args.m;
-    const float* b_p = args.b + static_cast<int64_t>(b_row<E>(n0 + b_rowi, args.n)) * K + a_kq;
-
-    f32x16 acc[2];
+    // Rows this wave streams: A blocks i = wave + 4j (16 rows each), B blocks likewise.
+    constexpr int kABlocks = kBMt / 16;            // 4 or 8
+    constexpr int kAPerWave = kABlocks / 4;        // 1 or 2
+    const float* a_src[kAPerWave];
+    const float* b_src[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int j = 0; j < kAPerWave; ++j) {
+        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+        const int64_t gr = m0 + row < args.m ? m0 + row : args.m - 1;
+        a_src[j] = args.a + gr * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    for (int j = 0; j < 2; ++j) {
+        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+        const int col = n0 + row < args.n ? n0 + row : args.n - 1;
+        b_src[j] = args.b + static_cast<int64_t>(b_row<E>(col, args.n)) * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
+    auto issue_stage = [&](int k0, int buf) {
+#pragma unroll
+        for (int j = 0; j < kAPerWave; ++j)
+            lds_copy16(a_src[j] + k0, &a_s[buf][(wave + 4 * j) * 16 * kBK]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            lds_copy16(b_src[j] + k0, &b_s[buf][(wave + 4 * j) * 16 * kBK]);
+    };
 
-    float4 ra0, ra1, rb;
-    auto load_stage = [&](int k0) {
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        ra0 = a_ok0 ? *reinterpret_cast<const float4*>(a_p0 + k0) : z;
-        ra1 = a_ok1 ? *reinterpret_cast<const float4*>(a_p1 + k0) : z;
-        rb = *reinterpret_cast<const float4*>(b_p + k0);
-    };
-    auto store_stage = [&](int buf) {
-        a_s[buf][a_kq + 0][a_row] = ra0.x; a_s[buf][a_kq + 1][a_row] = ra0.y;
-        a_s[buf][a_kq + 2][a_row] = ra0.z; a_s[buf][a_kq + 3][a_row] = ra0.w;
-        a_s[buf][a_kq + 0][a_row + 64] = ra1.x; a_s[buf][a_kq + 1][a_row + 64] = ra1.y;
-        a_s[buf][a_kq + 2][a_row + 64] = ra1.z; a_s[buf][a_kq + 3][a_row + 64] = ra1.w;
-        b_s[buf][a_kq + 0][b_rowi] = rb.x; b_s[buf][a_kq + 1][b_rowi] = rb.y;
-        b_s[buf][a_kq + 2][b_rowi] = rb.z; b_s[buf][a_kq + 3][b_rowi] = rb.w;
-    };
+    f32x16 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Operand read offsets (floats) inside a tile for this lane: row, pieces 2h and 2h+1.
+    const int h = lane >> 5;
+    int a_off[MI][2], b_off[2][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+        const int r = wm * 32 * MI + 32 * i + (lane & 31);
+        a_off[i][0] = tile_offset(r, 2 * h);
+        a_off[i][1] = tile_offset(r, 2 * h + 1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + 32 * j + (lane & 31);
+        b_off[j][0] = tile_offset(r, 2 * h);
+        b_off[j][1] = tile_offset(r, 2 * h + 1);
+    }
 
     const int stages = K / kBK;
-    load_stage(0);
-    store_stage(0);
+    issue_stage(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int s = 0; s < stages; ++s) {
         const int buf = s & 1;
-        if (s + 1 < stages) load_stage((s + 1) * kBK);
+        if (s + 1 < stages) issue_stage((s + 1) * kBK, buf ^ 1);
+        f32x4 av[MI][2], bv[2][2];
 #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 2) {
-            const float a = a_s[buf][kk + (lane >> 5)][wave * 32 + (lane & 31)];
-            const float b0 = b_s[buf][kk + (lane >> 5)][(lane & 31)];
-            const float b1 = b_s[buf][kk + (lane >> 5)][32 + (lane & 31)];
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b0, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b1, acc[1], 0, 0, 0);
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) av[i][q] = *reinterpret_cast<const f32x4*>(&a_s[buf][a_off[i][q]]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) bv[j][q] = *reinterpret_cast<const f32x4*>(&b_s[buf][b_off[j][q]]);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3], bv[j][kk >> 2][kk & 3],
+                                                                   acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < stages) store_stage(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);  // next stage's tiles have landed in LDS
         __syncthreads();
     }
+    if (!group_valid) return;
 
-    // Epilogue: lane holds columns j (tile 0) and j+32 (tile 1) for 16 rows.
+    // Epilogue: for 32-row subtile i, lane holds columns c (acc[i][0]) and c + 32
+    // (acc[i][1]) of the wave's 64-column group for 16 rows.
     const int j = lane & 31;
+    const int g0 = n0 + wn * 64;  // first column of the group
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wave * 32 + mfma32_row(lane, r);
-        if (row >= args.m) continue;
-        const float lo = acc[0][r];
-        const float hi = acc[1][r];
-        if constexpr (E == GemmEpilogue::kStore) {
-            args.c[row * args.n + n0 + j] = lo;
-            args.c[row * args.n + n0 + 32 + j] = hi;
-        } else if constexpr (E == GemmEpilogue::kResidual) {
-            const int64_t i0 = row * args.n + n0 + j;
-            args.c[i0] = args.residual[i0] + lo;
-            args.c[i0 + 32] = args.residual[i0 + 32] + hi;
-        } else if constexpr (E == GemmEpilogue::kSwiglu) {
-            const int half = args.n / 2;
-            args.c[row * half + (n0 >> 1) + j] = silu(lo) * hi;
-        } else {  // kQkvRope: tile = one head; columns j / j+32 are the RoPE pair.
-            const int head = n0 / kHeadDim;
-            if (head < kQHeads + kKVHeads) {
-                const float* cr = args.rope_cos + row * kHeadDim;
-                const float* sr = args.rope_sin + row * kHeadDim;
-                const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
-                const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
-                float* dst = head < kQHeads
-                                 ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
-                                 : args.key_cache + (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
-                dst[j] = qlo;
-                dst[j + 32] = qhi;
-            } else {
-                float* dst = args.value_cache +
-                             (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
-                dst[j] = lo;
-                dst[j + 32] = hi;
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + wm * 32 * MI + 32 * i + mfma32_row(lane, r);
+            if (row >= args.m) continue;
+            const float lo = acc[i][0][r];
+            const float hi = acc[i][1][r];
+            if constexpr (E == GemmEpilogue::kStore) {
+                args.c[row * args.n + g0 + j] = lo;
+                args.c[row * args.n + g0 + 32 + j] = hi;
+            } else if constexpr (E == GemmEpilogue::kResidual) {
+                const int64_t i0 = row * args.n + g0 + j;
+                args.c[i0] = args.residual[i0] + lo;
+                args.c[i0 + 32] = args.residual[i0 + 32] + hi;
+            } else if constexpr (E == GemmEpilogue::kSwiglu) {
+                const int half = args.n / 2;
+                args.c[row * half + (g0 >> 1) + j] = silu(lo) * hi;
+            } else {  // kQkvRope: the column group is one head; columns j / j+32 are the RoPE pair.
+                const int head = g0 / kHeadDim;
+                if (head < kQHeads + kKVHeads) {
+                    const float* cr = args.rope_cos + row * kHeadDim;
+                    const float* sr = args.rope_sin + row * kHeadDim;
+                    const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
+                    const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
+                    float* dst = head < kQHeads
+                                     ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
+                                     : args.key_cache +
+                                           (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
+                    dst[j] = qlo;
+                    dst[j + 32] = qhi;
+                } else {
+                    float* dst = args.value_cache +
+                                 (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
+                    dst[j] = lo;
+                    dst[j + 32] = hi;
+                }
             }
         }
     }
@@ -322,23 +373,36 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
-    if (args.k % kBK != 0 || args.n % kBN != 0 || args.m <= 0) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(args.n / kBN), static_cast<unsigned>((args.m + kBM - 1) / kBM));
+    if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
+    if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
+    if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
+    // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles.
+    const unsigned gx = static_cast<unsigned>((args.n + kBN - 1) / kBN);
+    const bool big = static_cast<int64_t>(gx) * ((args.m + 127) / 128) >= 512;
+    const dim3 grid(gx, static_cast<unsigned>(big ? (args.m + 127) / 128 : (args.m + 63) / 64));
+    const dim3 block(kGemmThreads);
+#define FLUX_LAUNCH_GEMM(E)                                                                    \
+    do {                                                                                       \
+        if (big)                                                                               \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 2>), grid, block, 0, stream, args);             \
+        else                                                                                   \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 1>), grid, block, 0, stream, args);             \
+    } while (0)
     switch (epilogue) {
         case GemmEpilogue::kStore:
-            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kStore>, grid, dim3(kGemmThreads), 0, stream, args);
+            FLUX_LAUNCH_GEMM(GemmEpilogue::kStore);
             break;
         case GemmEpilogue::kResidual:
-            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kResidual>, grid, dim3(kGemmThreads), 0, stream, args);
+            FLUX_LAUNCH_GEMM(GemmEpilogue::kResidual);
             break;
         case GemmEpilogue::kSwiglu:
-            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kSwiglu>, grid, dim3(kGemmThreads), 0, stream, args);
+            FLUX_LAUNCH_GEMM(GemmEpilogue::kSwiglu);
             break;
         case GemmEpilogue::kQkvRope:
-            if (args.n != kQKV) return hipErrorInvalidValue;
-            hipLaunchKernelGGL(gemm_kernel<GemmEpilogue::kQkvRope>, grid, dim3(kGemmThreads), 0, stream, args);
+            FLUX_LAUNCH_GEMM(GemmEpilogue::kQkvRope);
             break;
     }
+#undef FLUX_LAUNCH_GEMM
     return hipGetLastError();
 }
 
