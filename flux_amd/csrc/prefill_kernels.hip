@@ -232,8 +232,8 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
                                                                          const float* __restrict__ value_cache,
                                                                          int64_t seq, int64_t capacity, float scale,
                                                                          float* __restrict__ out_rows) {
-    __shared__ float k_s[kKTile][kHeadDim + kKVPad];
-    __shared__ float v_s[kKTile][kHeadDim + kKVPad];
+    __shared__ __align__(16) float k_s[kKTile][kHeadDim + kKVPad];
+    __shared__ __align__(16) float v_s[kKTile][kHeadDim + kKVPad];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -246,13 +246,22 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
     const int64_t row_base = q0 + wave * 16;
     const int64_t my_row = row_base + (lane & 15);  // query row of this lane in S^T / O^T layouts
 
-    // B operand of S^T = K Q^T: lane holds Q[row = lane%16][d = 4s + lane/16].
+    // B operand of S^T = K Q^T.  MFMA instruction s pairs k-slot jg = lane/16 with
+    // dim 16 jg + s, so qreg[s] = Q[row = lane%16][16 jg + s] and a lane reads its 16
+    // K values of a key row with four ds_read_b128.
+    const int jg = lane >> 4;
     float qreg[16];
     {
         const int64_t r = my_row < seq ? my_row : seq - 1;
-        const float* qp = q + (static_cast<int64_t>(h) * seq + r) * kHeadDim;
+        const float* qp = q + (static_cast<int64_t>(h) * seq + r) * kHeadDim + 16 * jg;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) qreg[s] = qp[4 * s + (lane >> 4)];
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const float4 v = *reinterpret_cast<const float4*>(qp + 4 * s4);
+            qreg[4 * s4] = v.x;
+            qreg[4 * s4 + 1] = v.y;
+            qreg[4 * s4 + 2] = v.z;
+            qreg[4 * s4 + 3] = v.w;
+        }
     }
 
     const float* kg = key_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
@@ -291,23 +300,35 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
         f32x4 s_acc[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
+            const float* krow = &k_s[kb * 16 + (lane & 15)][16 * jg];
+            f32x4 kr[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) kr[t] = *reinterpret_cast<const f32x4*>(krow + 4 * t);
             s_acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const float a = k_s[kb * 16 + (lane & 15)][4 * s + (lane >> 4)];
-                s_acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qreg[s], s_acc[kb], 0, 0, 0);
-            }
+            for (int s = 0; s < 16; ++s)
+                s_acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s >> 2][s & 3], qreg[s], s_acc[kb], 0, 0, 0);
         }
         // Scale + causal mask; lane holds keys k0 + 16kb + 4(lane/16) + r for row my_row.
         float tile_max = -INFINITY;
+        if (k0 + kKTile - 1 <= row_base) {  // every key of the tile precedes every query of the wave
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+            for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t key = k0 + 16 * kb + 4 * (lane >> 4) + r;
-                const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale2 : -INFINITY;
-                s_acc[kb][r] = v;
-                tile_max = fmaxf(tile_max, v);
+                for (int r = 0; r < 4; ++r) {
+                    s_acc[kb][r] *= scale2;
+                    tile_max = fmaxf(tile_max, s_acc[kb][r]);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t key = k0 + 16 * kb + 4 * (lane >> 4) + r;
+                    const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale2 : -INFINITY;
+                    s_acc[kb][r] = v;
+                    tile_max = fmaxf(tile_max, v);
+                }
             }
         }
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
