@@ -135,8 +135,9 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_gate_up_swiglu_rows_f32", ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int64, _stream]),
     ("flux_qkv_rope_cache_rows_f32", ctypes.c_int,
      [_vp, _vp, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int64, _stream]),
+    ("flux_prefill_attention_workspace_bytes", ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
     ("flux_prefill_attention_f32", ctypes.c_int,
-     [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _vp, _stream]),
+     [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _vp, _vp, _stream]),
     ("flux_embedding_gather_f32", ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _stream]),
 ]
 

@@ -372,12 +372,23 @@ int flux_qkv_rope_cache_rows_f32(const float* x, const float* packed_qkv, const 
     return from_hip(flux::launch_gemm(args, flux::GemmEpilogue::kQkvRope, stream), "flux_qkv_rope_cache_rows_f32");
 }
 
+int flux_prefill_attention_workspace_bytes(int64_t seq, int64_t* bytes) {
+    if (!bytes || seq <= 0 || seq > FLUX_MAX_CAPACITY)
+        return invalid("flux_prefill_attention_workspace_bytes: invalid argument");
+    *bytes = static_cast<int64_t>(flux::prefill_attention_workspace_floats(seq) * sizeof(float));
+    return FLUX_OK;
+}
+
 int flux_prefill_attention_f32(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
-                               int64_t capacity, float scale, float* out_rows, hipStream_t stream) {
+                               int64_t capacity, float scale, float* workspace, float* out_rows, hipStream_t stream) {
     if (!q || !key_cache || !value_cache || !out_rows || seq <= 0 || seq > capacity || capacity > FLUX_MAX_CAPACITY)
         return invalid("flux_prefill_attention_f32: invalid argument");
-    return from_hip(flux::launch_prefill_attention(q, key_cache, value_cache, seq, capacity, scale, out_rows, stream),
-                    "flux_prefill_attention_f32");
+    if (flux::prefill_attention_workspace_floats(seq) > 0 && !workspace)
+        return invalid("flux_prefill_attention_f32: this prompt length needs a workspace "
+                       "(flux_prefill_attention_workspace_bytes)");
+    return from_hip(
+        flux::launch_prefill_attention(q, key_cache, value_cache, seq, capacity, scale, workspace, out_rows, stream),
+        "flux_prefill_attention_f32");
 }
 
 int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq, float* hidden,

@@ -100,8 +100,12 @@ struct GemmArgs {
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream);
 
+// Workspace (floats) of launch_prefill_attention for a prompt of `seq` tokens (0 when
+// every query tile fits in one key chunk).
+size_t prefill_attention_workspace_floats(int64_t seq);
 hipError_t launch_prefill_attention(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
-                                    int64_t capacity, float scale, float* out_rows, hipStream_t stream);
+                                    int64_t capacity, float scale, float* workspace, float* out_rows,
+                                    hipStream_t stream);
 
 hipError_t launch_embedding_gather(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
                                    float* hidden, hipStream_t stream);

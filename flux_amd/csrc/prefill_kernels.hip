@@ -221,26 +221,54 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA prefill attention.
+// Causal GQA prefill attention.  The keys of a query tile are split into chunks of
+// at most kChunkTiles key tiles; every (query tile, head, chunk) is one block, so
+// no block streams more than 2048 keys (the causal tail would otherwise be one
+// block per head walking all S keys).  A query tile with one chunk writes its rows
+// directly; longer ones write (o, m, l) partials that prefill_attention_merge_kernel
+// combines (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu splits the keys
+// into partitions and merges them the same way).
 constexpr int kQTile = 64;
 constexpr int kKTile = 64;
 constexpr int kAttnThreads = 256;
 constexpr int kKVPad = 4;
+constexpr int kChunkTiles = 32;
+constexpr int kPartialRow = kHeadDim + 2;  // o[64], m, l
+
+__host__ __device__ __forceinline__ int64_t attn_q_tiles(int64_t seq) { return (seq + kQTile - 1) / kQTile; }
+__host__ __device__ __forceinline__ int64_t attn_max_chunks(int64_t seq) {
+    return (attn_q_tiles(seq) + kChunkTiles - 1) / kChunkTiles;
+}
+// Blocks of chunk c: query tiles qt >= c * kChunkTiles, times the query heads.
+__host__ __device__ __forceinline__ int64_t attn_chunk_blocks(int64_t seq, int64_t c) {
+    return (attn_q_tiles(seq) - c * kChunkTiles) * kQHeads;
+}
+// Partial slot of (qt, h, c) for query tiles with more than one chunk.
+__host__ __device__ __forceinline__ int64_t attn_partial_slot(int64_t seq, int64_t qt, int h, int64_t c) {
+    return ((qt - kChunkTiles) * kQHeads + h) * attn_max_chunks(seq) + c;
+}
 
 __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const float* __restrict__ q,
                                                                          const float* __restrict__ key_cache,
                                                                          const float* __restrict__ value_cache,
                                                                          int64_t seq, int64_t capacity, float scale,
+                                                                         float* __restrict__ workspace,
                                                                          float* __restrict__ out_rows) {
     __shared__ __align__(16) float k_s[kKTile][kHeadDim + kKVPad];
     __shared__ __align__(16) float v_s[kKTile][kHeadDim + kKVPad];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t q_tiles = (seq + kQTile - 1) / kQTile;
-    // Longest tiles first: block b -> q tile (q_tiles - 1 - b / 9), head b % 9.
-    const int64_t qt = q_tiles - 1 - blockIdx.x / kQHeads;
-    const int h = blockIdx.x % kQHeads;
+    const int64_t q_tiles = attn_q_tiles(seq);
+    // Block b -> chunk c (chunk-major), then q tile (longest first) and head.
+    int64_t idx = blockIdx.x;
+    int64_t chunk = 0;
+    while (idx >= attn_chunk_blocks(seq, chunk)) {
+        idx -= attn_chunk_blocks(seq, chunk);
+        ++chunk;
+    }
+    const int64_t qt = q_tiles - 1 - idx / kQHeads;
+    const int h = static_cast<int>(idx % kQHeads);
     const int g = h / kGroup;
     const int64_t q0 = qt * kQTile;
     const int64_t row_base = q0 + wave * 16;
@@ -276,7 +304,9 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
     const float scale2 = scale * kLog2e;  // scores in log2 units
     const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
     const int64_t k_tiles = last_key / kKTile + 1;
-    for (int64_t kt = 0; kt < k_tiles; ++kt) {
+    const int64_t kt_begin = chunk * kChunkTiles;
+    const int64_t kt_end = kt_begin + kChunkTiles < k_tiles ? kt_begin + kChunkTiles : k_tiles;
+    for (int64_t kt = kt_begin; kt < kt_end; ++kt) {
         const int64_t k0 = kt * kKTile;
         __syncthreads();
         // Stage K and V tiles (64 x 64 each): 1024 float4 per tile, 4 per thread.
@@ -366,7 +396,8 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
         }
     }
     // O^T accumulator: lane holds d = 16db + 4(lane/16) + r for row my_row.
-    if (my_row < seq) {
+    if (my_row >= seq) return;
+    if (k_tiles <= kChunkTiles) {
         const float inv = 1.0f / l_run;
         float* dst = out_rows + my_row * kHidden + h * kHeadDim;
 #pragma unroll
@@ -374,7 +405,62 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const f
 #pragma unroll
             for (int r = 0; r < 4; ++r) dst[16 * db + 4 * (lane >> 4) + r] = o_acc[db][r] * inv;
         }
+    } else {
+        float* dst = workspace + (attn_partial_slot(seq, qt, h, chunk) * kQTile + (my_row - q0)) * kPartialRow;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[16 * db + 4 * (lane >> 4) + r] = o_acc[db][r];
+        }
+        if (lane < 16) {
+            dst[kHeadDim] = m_run;  // log2 units
+            dst[kHeadDim + 1] = l_run;
+        }
     }
+}
+
+// Combines the chunk partials of query tiles with more than one chunk.  Block
+// ((qt - kChunkTiles) * 9 + h) * 16 + row group; thread t -> row 4 * group + t / 64,
+// dim t % 64.  All chunk loads of a thread are issued before the combine.
+constexpr int kMergeMaxChunks = 8;  // kMaxCapacity / (kChunkTiles * kKTile)
+
+__global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(const float* __restrict__ workspace,
+                                                                               int64_t seq,
+                                                                               float* __restrict__ out_rows) {
+    const int64_t tile_head = blockIdx.x / (kQTile / 4);
+    const int64_t qt = kChunkTiles + tile_head / kQHeads;
+    const int h = static_cast<int>(tile_head % kQHeads);
+    const int row = static_cast<int>(blockIdx.x % (kQTile / 4)) * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int d = threadIdx.x & 63;
+    const int64_t q0 = qt * kQTile;
+    if (q0 + row >= seq) return;
+    const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
+    const int chunks = static_cast<int>((last_key / kKTile + kChunkTiles) / kChunkTiles);
+    float o[kMergeMaxChunks], m[kMergeMaxChunks], l[kMergeMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+        if (c < chunks) {
+            const float* p = workspace + (attn_partial_slot(seq, qt, h, c) * kQTile + row) * kPartialRow;
+            o[c] = p[d];
+            m[c] = p[kHeadDim];
+            l[c] = p[kHeadDim + 1];
+        } else {
+            o[c] = 0.0f;
+            m[c] = -INFINITY;
+            l[c] = 0.0f;
+        }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) M = fmaxf(M, m[c]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kMergeMaxChunks; ++c) {
+        const float f = m[c] == -INFINITY ? 0.0f : fast_exp2(m[c] - M);
+        O = fmaf(o[c], f, O);
+        L = fmaf(l[c], f, L);
+    }
+    out_rows[(q0 + row) * kHidden + h * kHeadDim + d] = O / L;
 }
 
 __global__ void embedding_gather_kernel(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
@@ -427,13 +513,32 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     return hipGetLastError();
 }
 
+size_t prefill_attention_workspace_floats(int64_t seq) {
+    const int64_t long_tiles = attn_q_tiles(seq) - kChunkTiles;
+    if (long_tiles <= 0) return 0;
+    return static_cast<size_t>(long_tiles * kQHeads * attn_max_chunks(seq) * kQTile * kPartialRow);
+}
+
 hipError_t launch_prefill_attention(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
-                                    int64_t capacity, float scale, float* out_rows, hipStream_t stream) {
+                                    int64_t capacity, float scale, float* workspace, float* out_rows,
+                                    hipStream_t stream) {
     if (seq <= 0 || seq > capacity) return hipErrorInvalidValue;
-    const int64_t q_tiles = (seq + kQTile - 1) / kQTile;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(q_tiles * kQHeads)), dim3(kAttnThreads), 0,
-                       stream, q, key_cache, value_cache, seq, capacity, scale, out_rows);
-    return hipGetLastError();
+    if (prefill_attention_workspace_floats(seq) > 0 && workspace == nullptr) return hipErrorInvalidValue;
+    if (attn_max_chunks(seq) > kMergeMaxChunks) return hipErrorInvalidValue;
+    int64_t blocks = 0;
+    for (int64_t c = 0; c < attn_max_chunks(seq); ++c) blocks += attn_chunk_blocks(seq, c);
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kAttnThreads), 0, stream, q,
+                       key_cache, value_cache, seq, capacity, scale, workspace, out_rows);
+    hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return st;
+    const int64_t long_tiles = attn_q_tiles(seq) - kChunkTiles;
+    if (long_tiles > 0) {
+        hipLaunchKernelGGL(prefill_attention_merge_kernel,
+                           dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / 4))), dim3(kAttnThreads), 0,
+                           stream, workspace, seq, out_rows);
+        st = hipGetLastError();
+    }
+    return st;
 }
 
 hipError_t launch_embedding_gather(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,

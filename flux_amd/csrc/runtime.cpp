@@ -413,6 +413,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     const size_t o_q = take(sizeof(float) * s * kQHeads * kHeadDim);
     const size_t o_attn = take(sizeof(float) * s * kHidden);
     const size_t o_swiglu = take(sizeof(float) * s * kInter);
+    const size_t o_attn_ws = take(sizeof(float) * prefill_attention_workspace_floats(s));
     const size_t o_final = take(sizeof(float) * kHidden);
     const size_t o_logits = take(sizeof(float) * vocab_);
     const size_t o_token = take(sizeof(int64_t));
@@ -430,6 +431,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     query_ = reinterpret_cast<float*>(base + o_q);
     attn_rows_ = reinterpret_cast<float*>(base + o_attn);
     swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
+    attn_workspace_ = reinterpret_cast<float*>(base + o_attn_ws);
     final_hidden_ = reinterpret_cast<float*>(base + o_final);
     logits_ = reinterpret_cast<float*>(base + o_logits);
     initial_token_ = reinterpret_cast<int64_t*>(base + o_token);
@@ -493,7 +495,8 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         qkv.value_cache = values;
         qkv.capacity = capacity_;
         check_hip(launch_gemm(qkv, GemmEpilogue::kQkvRope, stream), "launching QKV GEMM");
-        check_hip(launch_prefill_attention(query_, keys, values, seq_, capacity_, scales_[layer], attn_rows_, stream),
+        check_hip(launch_prefill_attention(query_, keys, values, seq_, capacity_, scales_[layer], attn_workspace_,
+                                           attn_rows_, stream),
                   "launching prefill attention");
         GemmArgs o{};
         o.a = attn_rows_;

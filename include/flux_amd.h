@@ -257,11 +257,18 @@ int flux_qkv_rope_cache_rows_f32(const float* x, const float* packed_qkv, const 
                                  int64_t rows, float* q_out, float* key_cache, float* value_cache, int64_t capacity,
                                  hipStream_t stream);
 
-/* Causal GQA prefill attention (FP32 MFMA, online softmax): q [9,seq,64], K/V
- * [3,capacity,64] -> out_rows [seq, 576].  Replaces streaming_prefill_gqa_cuda_fp32
- * (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu:423-460) + K15. */
+/* Workspace (bytes) flux_prefill_attention_f32 needs for a prompt of `seq` tokens: the
+ * split-key partials of long query tiles; 0 for seq <= 2048.  Counterpart of the
+ * reference's partition workspace size (test_streaming_prefill_gqa.cu:503-512). */
+int flux_prefill_attention_workspace_bytes(int64_t seq, int64_t* bytes);
+
+/* Causal GQA prefill attention (FP32 MFMA, online softmax, keys split in chunks of
+ * 2048 and merged): q [9,seq,64], K/V [3,capacity,64] -> out_rows [seq, 576].
+ * `workspace` may be NULL when flux_prefill_attention_workspace_bytes reports 0.
+ * Replaces streaming_prefill_gqa_cuda_fp32 (csrc/streaming_prefill_gqa/
+ * streaming_prefill_gqa_cuda.cu:423-460) + K15. */
 int flux_prefill_attention_f32(const float* q, const float* key_cache, const float* value_cache, int64_t seq,
-                               int64_t capacity, float scale, float* out_rows, hipStream_t stream);
+                               int64_t capacity, float scale, float* workspace, float* out_rows, hipStream_t stream);
 
 /* hidden[s] = embedding[ids[s]] (zero row when out of vocabulary).
  * Replaces embedding_gather_fp32_kernel (native_prefill_runtime_cuda.cu:85-103). */

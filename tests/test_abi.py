@@ -59,7 +59,7 @@ def test_version_and_empty_error():
     lambda lib: lib.flux_linear_f32(None, None, None, None, 4, 64, 16, None),
     lambda lib: lib.flux_gate_up_swiglu_rows_f32(None, None, None, 4, None),
     lambda lib: lib.flux_qkv_rope_cache_rows_f32(None, None, None, None, 4, None, None, None, 8, None),
-    lambda lib: lib.flux_prefill_attention_f32(None, None, None, 4, 8, 0.125, None, None),
+    lambda lib: lib.flux_prefill_attention_f32(None, None, None, 4, 8, 0.125, None, None, None),
     lambda lib: lib.flux_embedding_gather_f32(None, None, 10, 4, None, None),
     lambda lib: lib.flux_decode_create(None, None, None, 8, 0, None, None, None, None, None, None, None, None),
     lambda lib: lib.flux_prefill_create(None, None, None, 8, None, 4, None, None, None, None),
@@ -83,6 +83,15 @@ def test_shape_constraints_are_rejected():
     assert lib.flux_gqa_decode_workspace_bytes(16385, ctypes.byref(size)) == _native.FLUX_ERROR_INVALID_VALUE
     assert lib.flux_gqa_decode_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 85 * 3 * 3 * 66 * 4
+    assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
+    assert size.value == 0
+    assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
+    # 96 query tiles past the first chunk x 9 heads x 4 chunks x 64 rows x (64 + m + l) floats
+    assert size.value == 96 * 9 * 4 * 64 * 66 * 4
+    dummy = ctypes.c_void_p(16)
+    assert lib.flux_prefill_attention_f32(dummy, dummy, dummy, 4096, 4096, 0.125, None, dummy,
+                                          None) == _native.FLUX_ERROR_INVALID_VALUE
+    assert "workspace" in _native.last_error()
 
 
 def test_runtime_constructor_validation_messages():

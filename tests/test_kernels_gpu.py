@@ -299,14 +299,23 @@ def test_qkv_rope_cache_rows(gpu_device, rows, capacity):
     assert torch.all(kc[:, rows:] == 0) and torch.all(vc[:, rows:] == 0)
 
 
-@pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024)])
+def _attention_workspace(seq, device):
+    size = ctypes.c_int64()
+    _native.check(_lib().flux_prefill_attention_workspace_bytes(seq, ctypes.byref(size)))
+    return torch.empty(max(size.value // 4, 1), device=device)
+
+
+@pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024),
+                                          (2049, 2100), (4160, 4160)])
 def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
+    # 2049 and 4160 exercise the split-key path (query tiles past 2048 keys) and its merge.
     q = _randn(9, seq, D, seed=91).to(gpu_device)
     kc = _randn(3, capacity, D, seed=92).to(gpu_device)
     vc = _randn(3, capacity, D, seed=93).to(gpu_device)
     out = torch.empty(seq, H, device=gpu_device)
+    ws = _attention_workspace(seq, gpu_device)
     _native.check(_lib().flux_prefill_attention_f32(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), seq, capacity, 0.125,
-                                                    out.data_ptr(), _s(gpu_device)))
+                                                    ws.data_ptr(), out.data_ptr(), _s(gpu_device)))
     torch.cuda.synchronize()
     expected = ref.causal_attention(q.cpu(), kc.cpu(), vc.cpu(), 0.125)  # [9, seq, 64]
     _close(out.view(seq, 9, D).transpose(0, 1), expected, rtol=2e-4, atol=2e-5)
@@ -319,7 +328,7 @@ def test_prefill_attention_zero_query_prefix_mean(gpu_device):
     vc = _randn(3, capacity, D, seed=95).to(gpu_device)
     out = torch.empty(seq, H, device=gpu_device)
     _native.check(_lib().flux_prefill_attention_f32(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), seq, capacity, 0.125,
-                                                    out.data_ptr(), _s(gpu_device)))
+                                                    None, out.data_ptr(), _s(gpu_device)))
     torch.cuda.synchronize()
     prefix = vc.cpu().double().cumsum(dim=1) / torch.arange(1, capacity + 1).double()[None, :, None]
     expected = prefix[:, :seq].repeat_interleave(3, dim=0)
