@@ -139,6 +139,22 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_prefill_attention_f32", ctypes.c_int,
      [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _vp, _vp, _stream]),
     ("flux_embedding_gather_f32", ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _stream]),
+    ("flux_rope_f32", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+      ctypes.c_int64, _i64, _i64, _i64, _i64, _stream]),
+    ("flux_softmax_f32", ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _stream]),
+    ("flux_attention_score_softmax_f32", ctypes.c_int,
+     [_vp, _vp, _vp, ctypes.c_float, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64, _i64,
+      _stream]),
+    ("flux_packed_swiglu_f32", ctypes.c_int, [_vp, _vp, ctypes.c_int64, ctypes.c_int64, _stream]),
+    ("flux_packed_qkv_rope_cache_f32", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64,
+      _i64, _stream]),
+    ("flux_gqa_decode_attention_strided_workspace_bytes", ctypes.c_int,
+     [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64]),
+    ("flux_gqa_decode_attention_strided_f32", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_float, ctypes.c_int64, ctypes.c_int64,
+      ctypes.c_int64, ctypes.c_int64, _i64, _i64, _i64, _i64, _i64, _stream]),
 ]
 
 EXPORTED_SYMBOLS = tuple(name for name, _, _ in _PROTOTYPES)

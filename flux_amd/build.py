@@ -19,7 +19,7 @@ ROOT = os.path.dirname(PACKAGE)
 CSRC = os.path.join(PACKAGE, "csrc")
 LIB_DIR = os.path.join(PACKAGE, "lib")
 LIBRARY = os.path.join(LIB_DIR, "libflux_amd.so")
-SOURCES = ("decode_kernels.hip", "prefill_kernels.hip", "runtime.cpp", "capi.cpp")
+SOURCES = ("decode_kernels.hip", "prefill_kernels.hip", "eager_kernels.hip", "runtime.cpp", "capi.cpp")
 ARCH = os.environ.get("FLUX_AMD_ARCH", "gfx950")
 
 

@@ -5,6 +5,8 @@
 #include "flux_kernels.h"
 #include "runtime.h"
 
+#include <cmath>
+#include <cstdint>
 #include <new>
 #include <string>
 
@@ -214,7 +216,7 @@ void flux_prefill_destroy(flux_prefill* runtime) {
 // ---------------------------------------------------------------------------
 int flux_rmsnorm_f32(const float* x, const float* weight, float* out, int64_t rows, int64_t cols, float eps,
                      hipStream_t stream) {
-    if (!x || !weight || !out || rows <= 0 || cols <= 0 || cols > 65536 || !(eps > 0.0f))
+    if (!x || !weight || !out || rows <= 0 || cols <= 0 || cols > 65536 || !(eps > 0.0f) || !std::isfinite(eps))
         return invalid("flux_rmsnorm_f32: invalid argument");
     return from_hip(flux::launch_rmsnorm_rows(x, weight, out, rows, static_cast<int>(cols), eps, stream),
                     "flux_rmsnorm_f32");
@@ -223,7 +225,7 @@ int flux_rmsnorm_f32(const float* x, const float* weight, float* out, int64_t ro
 int flux_residual_rmsnorm_f32(const float* hidden, const float* residual, const float* weight, float* norm_out,
                               float* residual_out, int64_t rows, int64_t cols, float eps, hipStream_t stream) {
     if (!hidden || !residual || !weight || !norm_out || !residual_out || rows <= 0 || cols <= 0 || cols > 65536 ||
-        !(eps > 0.0f))
+        !(eps >= 0.0f) || !std::isfinite(eps))
         return invalid("flux_residual_rmsnorm_f32: invalid argument");
     return from_hip(flux::launch_residual_rmsnorm_rows(hidden, residual, weight, norm_out, residual_out, rows,
                                                        static_cast<int>(cols), eps, stream),
@@ -397,6 +399,157 @@ int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_
         return invalid("flux_embedding_gather_f32: invalid argument");
     return from_hip(flux::launch_embedding_gather(ids, embedding, vocab, seq, hidden, stream),
                     "flux_embedding_gather_f32");
+}
+
+// ---------------------------------------------------------------------------
+// Eager operators.
+
+namespace {
+bool nonnegative(const int64_t* values, int count) {
+    for (int i = 0; i < count; ++i)
+        if (values[i] < 0) return false;
+    return true;
+}
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+}  // namespace
+
+int flux_rope_f32(const float* query, const float* key, const float* cos, const float* sin, float* query_out,
+                  float* key_out, int64_t batch, int64_t query_heads, int64_t key_heads, int64_t seq,
+                  int64_t head_dim, int64_t rope_batch, const int64_t* query_strides, const int64_t* key_strides,
+                  const int64_t* cos_strides, const int64_t* sin_strides, hipStream_t stream) {
+    if (!query || !key || !cos || !sin || !query_out || !key_out || !query_strides || !key_strides || !cos_strides ||
+        !sin_strides)
+        return invalid("flux_rope_f32: null argument");
+    if (batch <= 0 || query_heads <= 0 || key_heads <= 0 || seq <= 0 || head_dim <= 0 || (head_dim & 1) ||
+        (rope_batch != 1 && rope_batch != batch))
+        return invalid("flux_rope_f32: invalid shape (head_dim must be even, rope batch 1 or batch)");
+    if (!nonnegative(query_strides, 4) || !nonnegative(key_strides, 4) || !nonnegative(cos_strides, 3) ||
+        !nonnegative(sin_strides, 3))
+        return invalid("flux_rope_f32: negative strides are unsupported");
+    flux::RopeShape shape{batch, query_heads, key_heads, seq, head_dim, rope_batch, {}, {}, {}, {}};
+    for (int i = 0; i < 4; ++i) {
+        shape.query_strides[i] = query_strides[i];
+        shape.key_strides[i] = key_strides[i];
+    }
+    for (int i = 0; i < 3; ++i) {
+        shape.cos_strides[i] = cos_strides[i];
+        shape.sin_strides[i] = sin_strides[i];
+    }
+    return from_hip(flux::launch_rope(query, key, cos, sin, query_out, key_out, shape, stream), "flux_rope_f32");
+}
+
+int flux_softmax_f32(const float* input, float* output, int64_t rows, int64_t width, hipStream_t stream) {
+    if (!input || !output || rows <= 0 || width <= 0) return invalid("flux_softmax_f32: invalid argument");
+    return from_hip(flux::launch_softmax(input, output, rows, width, stream), "flux_softmax_f32");
+}
+
+int flux_attention_score_softmax_f32(const float* scores, const float* mask, float* output, float scale,
+                                     int64_t batch, int64_t heads, int64_t query_length, int64_t key_length,
+                                     const int64_t* mask_sizes, const int64_t* mask_strides, hipStream_t stream) {
+    if (!scores || !mask || !output || !mask_sizes || !mask_strides || batch <= 0 || heads <= 0 ||
+        query_length <= 0 || key_length <= 0 || !std::isfinite(scale))
+        return invalid("flux_attention_score_softmax_f32: invalid argument");
+    const int64_t target[4] = {batch, heads, query_length, key_length};
+    int64_t strides[4];
+    for (int i = 0; i < 4; ++i) {
+        if (mask_sizes[i] != 1 && mask_sizes[i] != target[i])
+            return invalid("flux_attention_score_softmax_f32: mask is not broadcastable to scores");
+        if (mask_strides[i] < 0) return invalid("flux_attention_score_softmax_f32: negative mask strides");
+        strides[i] = mask_sizes[i] == 1 ? 0 : mask_strides[i];
+    }
+    return from_hip(flux::launch_attention_score_softmax(scores, mask, output, scale, batch, heads, query_length,
+                                                         key_length, strides, stream),
+                    "flux_attention_score_softmax_f32");
+}
+
+int flux_packed_swiglu_f32(const float* packed, float* output, int64_t rows, int64_t intermediate,
+                           hipStream_t stream) {
+    if (!packed || !output || rows <= 0 || intermediate <= 0)
+        return invalid("flux_packed_swiglu_f32: invalid argument");
+    return from_hip(flux::launch_packed_swiglu(packed, output, rows, intermediate, stream), "flux_packed_swiglu_f32");
+}
+
+int flux_packed_qkv_rope_cache_f32(const float* packed_qkv, const float* cos, const float* sin, float* key_cache,
+                                   float* value_cache, const int64_t* position, int64_t* cache_length,
+                                   float* query_out, int64_t capacity, int64_t packed_stride, int64_t cos_stride,
+                                   int64_t sin_stride, const int64_t* key_strides, const int64_t* value_strides,
+                                   hipStream_t stream) {
+    if (!packed_qkv || !cos || !sin || !key_cache || !value_cache || !position || !query_out || !key_strides ||
+        !value_strides || capacity <= 0)
+        return invalid("flux_packed_qkv_rope_cache_f32: invalid argument");
+    if (packed_stride <= 0 || cos_stride <= 0 || sin_stride <= 0 || !nonnegative(key_strides, 4) ||
+        !nonnegative(value_strides, 4))
+        return invalid("flux_packed_qkv_rope_cache_f32: strides must be positive");
+    flux::PackedQkvArgs args{packed_qkv, cos, sin, key_cache, value_cache, position, cache_length, query_out,
+                             capacity, packed_stride, cos_stride, sin_stride, {}, {}};
+    for (int i = 0; i < 4; ++i) {
+        args.key_strides[i] = key_strides[i];
+        args.value_strides[i] = value_strides[i];
+    }
+    return from_hip(flux::launch_packed_qkv_rope_cache(args, stream), "flux_packed_qkv_rope_cache_f32");
+}
+
+int flux_gqa_decode_attention_strided_workspace_bytes(int64_t query_heads, int64_t capacity, int64_t head_dim,
+                                                      int64_t* bytes) {
+    if (!bytes || query_heads <= 0 || capacity <= 0 || capacity > FLUX_MAX_CAPACITY || head_dim <= 0 ||
+        head_dim > 4096)
+        return invalid("flux_gqa_decode_attention_strided_workspace_bytes: invalid argument");
+    *bytes = static_cast<int64_t>(flux::gqa_strided_workspace_floats(query_heads, capacity, head_dim) * sizeof(float));
+    return FLUX_OK;
+}
+
+int flux_gqa_decode_attention_strided_f32(const float* query, const float* key_cache, const float* value_cache,
+                                          const float* mask, const int64_t* cache_length, float* output,
+                                          void* workspace, int64_t workspace_bytes, float scale, int64_t query_heads,
+                                          int64_t kv_heads, int64_t capacity, int64_t head_dim,
+                                          const int64_t* query_strides, const int64_t* key_strides,
+                                          const int64_t* value_strides, const int64_t* mask_sizes,
+                                          const int64_t* mask_strides, hipStream_t stream) {
+    if (!query || !key_cache || !value_cache || !output || !query_strides || !key_strides || !value_strides)
+        return invalid("flux_gqa_decode_attention_strided_f32: null argument");
+    if (query_heads <= 0 || kv_heads <= 0 || query_heads % kv_heads || query_heads > 65536 || capacity <= 0 ||
+        capacity > FLUX_MAX_CAPACITY || head_dim <= 0 || head_dim > 4096 || !std::isfinite(scale))
+        return invalid("flux_gqa_decode_attention_strided_f32: invalid shape or scale");
+    if (!nonnegative(query_strides, 4) || !nonnegative(key_strides, 4) || !nonnegative(value_strides, 4))
+        return invalid("flux_gqa_decode_attention_strided_f32: negative strides are unsupported");
+    int64_t needed = 0;
+    flux_gqa_decode_attention_strided_workspace_bytes(query_heads, capacity, head_dim, &needed);
+    if (needed > 0 && (!workspace || workspace_bytes < needed))
+        return invalid("flux_gqa_decode_attention_strided_f32: workspace missing or too small "
+                       "(flux_gqa_decode_attention_strided_workspace_bytes)");
+    flux::GqaStridedArgs args{};
+    args.q = query;
+    args.k = key_cache;
+    args.v = value_cache;
+    args.mask = mask;
+    args.cache_length = cache_length;
+    args.out = output;
+    args.workspace = static_cast<float*>(workspace);
+    args.scale = scale;
+    args.query_heads = static_cast<int>(query_heads);
+    args.groups = static_cast<int>(query_heads / kv_heads);
+    args.dim = static_cast<int>(head_dim);
+    args.chunks = flux::gqa_strided_chunks(capacity);
+    args.capacity = capacity;
+    for (int i = 0; i < 4; ++i) {
+        args.q_strides[i] = query_strides[i];
+        args.k_strides[i] = key_strides[i];
+        args.v_strides[i] = value_strides[i];
+    }
+    if (mask) {
+        if (!mask_sizes || !mask_strides)
+            return invalid("flux_gqa_decode_attention_strided_f32: mask needs sizes and strides");
+        const int64_t target[4] = {1, query_heads, 1, capacity};
+        for (int i = 0; i < 4; ++i) {
+            if (mask_sizes[i] != 1 && mask_sizes[i] != target[i])
+                return invalid("flux_gqa_decode_attention_strided_f32: mask is not broadcastable");
+            if (mask_strides[i] < 0) return invalid("flux_gqa_decode_attention_strided_f32: negative mask strides");
+            args.mask_strides[i] = mask_sizes[i] == 1 ? 0 : mask_strides[i];
+        }
+    }
+    args.vec = key_strides[3] == 1 && (head_dim & 3) == 0 && (key_strides[1] & 3) == 0 && (key_strides[2] & 3) == 0 &&
+               aligned16(key_cache);
+    return from_hip(flux::launch_gqa_strided(args, stream), "flux_gqa_decode_attention_strided_f32");
 }
 
 }  // extern "C"

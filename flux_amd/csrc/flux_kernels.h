@@ -110,4 +110,69 @@ hipError_t launch_prefill_attention(const float* q, const float* key_cache, cons
 hipError_t launch_embedding_gather(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
                                    float* hidden, hipStream_t stream);
 
+// ---- eager operators (torch.ops.flux.*) ----
+struct RopeShape {
+    int64_t batch;
+    int64_t query_heads;
+    int64_t key_heads;
+    int64_t seq;
+    int64_t head_dim;
+    int64_t rope_batch;         // 1 (broadcast) or batch
+    int64_t query_strides[4];   // [B, H, S, D] element strides
+    int64_t key_strides[4];
+    int64_t cos_strides[3];     // [B, S, D]
+    int64_t sin_strides[3];
+};
+hipError_t launch_rope(const float* query, const float* key, const float* cos_table, const float* sin_table,
+                       float* query_out, float* key_out, const RopeShape& shape, hipStream_t stream);
+
+hipError_t launch_softmax(const float* input, float* output, int64_t rows, int64_t width, hipStream_t stream);
+// mask_strides: element strides of the mask over [B, H, Q, K], 0 on broadcast dimensions.
+hipError_t launch_attention_score_softmax(const float* scores, const float* mask, float* output, float scale,
+                                          int64_t batch, int64_t heads, int64_t query_length, int64_t key_length,
+                                          const int64_t mask_strides[4], hipStream_t stream);
+hipError_t launch_packed_swiglu(const float* packed, float* out, int64_t rows, int64_t inter, hipStream_t stream);
+
+struct PackedQkvArgs {
+    const float* packed;      // [960], element stride packed_stride
+    const float* cos;         // [64], element stride cos_stride
+    const float* sin;
+    float* key_cache;         // [1, 3, capacity, 64] with key_strides
+    float* value_cache;
+    const int64_t* position;  // cache row to write
+    int64_t* cache_length;    // NULL or receives position + 1
+    float* query_out;         // [9, 64] contiguous
+    int64_t capacity;
+    int64_t packed_stride;
+    int64_t cos_stride;
+    int64_t sin_stride;
+    int64_t key_strides[4];
+    int64_t value_strides[4];
+};
+hipError_t launch_packed_qkv_rope_cache(const PackedQkvArgs& args, hipStream_t stream);
+
+struct GqaStridedArgs {
+    const float* q;                // [1, Hq, 1, D] with q_strides
+    const float* k;                // [1, Hkv, capacity, D] with k_strides
+    const float* v;
+    const float* mask;             // NULL or broadcast [1|1, 1|Hq, 1, 1|capacity]
+    const int64_t* cache_length;   // NULL (= capacity) or device scalar, clamped to [1, capacity]
+    float* out;                    // [Hq, D] contiguous
+    float* workspace;              // gqa_strided_workspace_floats() floats (unused for one chunk)
+    float scale;
+    int query_heads;
+    int groups;                    // Hq / Hkv
+    int dim;
+    int chunks;                    // gqa_strided_chunks(capacity)
+    int vec;                       // K rows contiguous, 16-byte aligned, dim % 4 == 0
+    int64_t capacity;
+    int64_t q_strides[4];
+    int64_t k_strides[4];
+    int64_t v_strides[4];
+    int64_t mask_strides[4];       // 0 on broadcast dimensions
+};
+int gqa_strided_chunks(int64_t capacity);
+size_t gqa_strided_workspace_floats(int64_t query_heads, int64_t capacity, int64_t head_dim);
+hipError_t launch_gqa_strided(const GqaStridedArgs& args, hipStream_t stream);
+
 }  // namespace flux

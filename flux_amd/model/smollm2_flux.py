@@ -4,14 +4,16 @@ Drop-in for ``flux.model.smollm2_flux`` (``/root/reference/flux/model/smollm2_fl
 same category names and dependency rules (:58-80, :900-935), same validation
 (:790-810), same packed parameters that the native runtimes consume
 (``self_attn.packed_qkv.weight`` = cat(q, k, v) ``[960, 576]`` (:325-338) and
-``mlp.gate_up_proj.weight`` = cat(gate, up) ``[3072, 576]`` (:151-165)), and the
-same state-dict transparency hooks (:167-214, :339-391).
+``mlp.gate_up_proj.weight`` = cat(gate, up) ``[3072, 576]`` (:151-165)), the
+same state-dict transparency hooks (:167-214, :339-391) and the same eager
+forward (:216-262, :422-683, :740-787): RMSNorm, residual RMSNorm, RoPE,
+attention-score softmax, packed SwiGLU, the StaticCache one-token
+packed-QKV/RoPE/cache step and one-token GQA decode attention run as
+``torch.ops.flux`` kernels (``flux_amd.ops``, HIP on gfx950).  Those operators
+have no CPU kernel, so an enabled model computes on ROCm GPU tensors only.
 
-Scope note: in this build the hot path is the native runtime
-(``flux_amd.runtime``).  The eager forward of the replaced modules computes
-with stock torch ops in Hugging Face's order (so ``model(...)`` keeps working,
-e.g. for ``NativeSmolLM2Decode.capture``'s eager prefill); the reference's eager
-custom-op set (``torch.ops.flux.*``) is not part of this build's hot path.
+The reference's cuBLASLt decode projections (category ``cublaslt_projection``)
+map to this build's decode GEMV kernel (``flux_amd.ops.decode_projection_out``).
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ from typing import Any
 import torch
 from torch import nn
 from torch.nn import functional as F
+from transformers import StaticCache
 from transformers.models.llama.modeling_llama import (
     LlamaAttention,
     LlamaDecoderLayer,
@@ -29,10 +32,27 @@ from transformers.models.llama.modeling_llama import (
     LlamaMLP,
     LlamaRMSNorm,
     apply_rotary_pos_emb,
-    eager_attention_forward,
+    repeat_kv,
 )
 
 from flux_amd import _native
+from flux_amd.ops import (
+    attention_score_softmax_native,
+    decode_projection_out,
+    gqa_decode_attention_native,
+    gqa_decode_attention_native_out,
+    packed_gate_up_swiglu_native_out,
+    packed_qkv_rope_cache_native,
+    packed_qkv_rope_cache_native_out,
+    packed_swiglu_native,
+    packed_swiglu_native_out,
+    residual_rmsnorm_native,
+    residual_rmsnorm_native_out,
+    rms_norm_native,
+    rms_norm_native_out,
+    rope_native,
+    softmax_native,
+)
 
 FLUX_OPERATOR_CATEGORIES = frozenset({"rmsnorm", "residual_rmsnorm", "rope", "softmax"})
 FLUX_PACKED_MLP_CATEGORY = "mlp"
@@ -53,6 +73,18 @@ _SUPPORTED_OPERATOR_CATEGORIES = FLUX_OPERATOR_CATEGORIES | {
 }
 # The complete retained configuration the native runtimes require.
 FINAL_FLUX_OPERATOR_CATEGORIES = _SUPPORTED_OPERATOR_CATEGORIES
+# One-token StaticCache paths need capacity above the single-chunk size
+# (reference smollm2_flux.py:81).
+_GQA_DECODE_GRAPH_MINIMUM_CAPACITY = 513
+# Decode projections served by the GEMV kernel (reference :86-97 lists the same shapes).
+_DECODE_PROJECTION_SHAPES = frozenset({(960, 576), (576, 576)})
+
+
+def _decode_projection_out(input: torch.Tensor, weight: torch.Tensor, output: torch.Tensor) -> torch.Tensor:
+    """Exact-shape decode projection dispatch (reference ``_cublaslt_decode_projection_out``, :100-116)."""
+    if tuple(weight.shape) not in _DECODE_PROJECTION_SHAPES:
+        return F.linear(input, weight)
+    return decode_projection_out(input, weight, output)
 
 
 def native_library_is_available() -> bool:
@@ -106,17 +138,32 @@ class FluxPackedLlamaMLP(nn.Module):
         state_dict[key] = torch.cat((state_dict.pop(gate_key), state_dict.pop(up_key)), dim=0)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        gate, up = F.linear(hidden_states, self.gate_up_proj.weight).chunk(2, dim=-1)
+        scratch = getattr(self, "_flux_decode_scratch", None)
+        if self.fuse_gate_up_swiglu and scratch is not None:
+            return self.down_proj(packed_gate_up_swiglu_native_out(hidden_states, self.gate_up_proj.weight,
+                                                                   scratch.swiglu_output))
+        gate_up = self.gate_up_proj(hidden_states)
+        if self.use_packed_swiglu:
+            if scratch is not None:
+                return self.down_proj(packed_swiglu_native_out(gate_up, scratch.swiglu_output))
+            return self.down_proj(packed_swiglu_native(gate_up))
+        gate, up = gate_up.chunk(2, dim=-1)
         return self.down_proj(self.act_fn(gate) * up)
 
 
 class FluxRMSNorm(LlamaRMSNorm):
-    """RMSNorm sharing the source Parameter (keeps names and weight tying)."""
+    """RMSNorm on ``flux::rmsnorm`` sharing the source Parameter (keeps names and weight tying)."""
 
     def __init__(self, source: LlamaRMSNorm) -> None:
         nn.Module.__init__(self)
         self.weight = source.weight
         self.variance_epsilon = source.variance_epsilon
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        scratch = getattr(self, "_flux_decode_scratch", None)
+        if scratch is not None:
+            return rms_norm_native_out(hidden_states, self.weight, self.variance_epsilon, scratch.norm_output)
+        return rms_norm_native(hidden_states, self.weight, self.variance_epsilon)
 
 
 class FluxLlamaAttention(LlamaAttention):
@@ -206,20 +253,124 @@ class FluxLlamaAttention(LlamaAttention):
                 self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2),
                 self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2))
 
+    def _static_decode_cache(self, hidden_states: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                             attention_mask: torch.Tensor | None, cache_layer: Any, cache_length: Any,
+                             kwargs: dict[str, Any]) -> bool:
+        """Whether one token can take the fused packed-QKV/RoPE/cache step (reference :437-487)."""
+        if not (self.use_packed_qkv_rope_cache and cache_layer is not None
+                and getattr(cache_layer, "is_initialized", False)):
+            return False
+        keys, values = getattr(cache_layer, "keys", None), getattr(cache_layer, "values", None)
+        if keys is None or values is None or cache_length is None:
+            return False
+        device = hidden_states.device
+        return (tuple(hidden_states.shape) == (1, 1, 576) and hidden_states.dtype == torch.float32
+                and device.type == "cuda" and tuple(cos.shape) == tuple(sin.shape) == (1, 1, 64)
+                and cos.dtype == sin.dtype == torch.float32 and cos.device == sin.device == device
+                and self.query_width == 576 and self.key_width == self.value_width == 192
+                and self.query_heads == 9 and self.key_value_heads == 3 and self.head_dim == 64
+                and keys.shape == values.shape and keys.shape[0] == 1 and keys.shape[1] == 3
+                and _GQA_DECODE_GRAPH_MINIMUM_CAPACITY <= keys.shape[2] <= 16384 and keys.shape[3] == 64
+                and keys.dtype == values.dtype == torch.float32 and keys.device == values.device == device
+                and cache_length.shape == () and cache_length.dtype == torch.int64 and cache_length.device == device
+                and (attention_mask is None or (
+                    attention_mask.ndim == 4 and attention_mask.dtype == torch.float32
+                    and attention_mask.device == device
+                    and all(m in (1, t) for m, t in zip(attention_mask.shape, (1, 9, 1, keys.shape[2])))))
+                and not kwargs.get("output_attentions", False))
+
+    def _gqa_decode_applies(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                            attention_mask: torch.Tensor | None, cache_length: Any, past_key_values: Any,
+                            kwargs: dict[str, Any]) -> bool:
+        """Whether one query token takes flux::gqa_decode_attention (reference :540-579)."""
+        return (self.use_gqa_decode_attention and past_key_values is not None
+                and query.shape[0] == 1 and query.shape[-2] == 1
+                and query.dtype == key.dtype == value.dtype == torch.float32
+                and query.ndim == key.ndim == value.ndim == 4 and key.shape == value.shape
+                and query.shape[0] == key.shape[0] and query.shape[-1] == key.shape[-1] and key.shape[1] > 0
+                and query.shape[1] % key.shape[1] == 0 and key.shape[-2] <= 16384
+                and (cache_length is None or key.shape[-2] >= _GQA_DECODE_GRAPH_MINIMUM_CAPACITY)
+                and (attention_mask is None or (
+                    attention_mask.ndim == 4 and attention_mask.dtype == torch.float32
+                    and attention_mask.device == query.device
+                    and all(m in (1, t) for m, t in zip(attention_mask.shape,
+                                                        (query.shape[0], query.shape[1], 1, key.shape[-2])))))
+                and not kwargs.get("output_attentions", False))
+
     def forward(self, hidden_states: torch.Tensor, position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
                 attention_mask: torch.Tensor | None = None, past_key_values: Any | None = None,
-                **kwargs: Any) -> tuple[torch.Tensor, torch.Tensor]:
+                **kwargs: Any) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """Flux attention (reference ``FluxLlamaAttention.forward``, :422-683)."""
         if position_embeddings is None:
             raise ValueError("position_embeddings must be provided")
-        input_shape = hidden_states.shape[:-1]
-        query, key, value = self.project_qkv(hidden_states)
         cos, sin = position_embeddings
-        query, key = apply_rotary_pos_emb(query, key, cos, sin)
-        if past_key_values is not None:
-            key, value = past_key_values.update(key, value, self.layer_idx)
-        out, weights = eager_attention_forward(self, query, key, value, attention_mask, dropout=0.0,
-                                               scaling=self.scaling)
-        out = out.reshape(*input_shape, -1).contiguous()
+        input_shape = hidden_states.shape[:-1]
+        cache_length = None
+        cache_layer = None
+        fused_post_qkv = False
+        if isinstance(past_key_values, StaticCache):
+            cache_layer = past_key_values.layers[self.layer_idx]
+            cache_length = getattr(cache_layer, "cumulative_length", None)
+        scratch = getattr(self, "_flux_decode_scratch", None)
+        if self._static_decode_cache(hidden_states, cos, sin, attention_mask, cache_layer, cache_length, kwargs):
+            if (self.use_cublaslt_projection and scratch is not None
+                    and getattr(scratch, "qkv_projection_output", None) is not None):
+                packed = _decode_projection_out(hidden_states, self.packed_qkv.weight, scratch.qkv_projection_output)
+            else:
+                packed = self.packed_qkv(hidden_states)
+            if scratch is None:
+                query = packed_qkv_rope_cache_native(packed, cos, sin, cache_layer.keys, cache_layer.values,
+                                                     cache_length)
+            else:
+                query = packed_qkv_rope_cache_native_out(packed, cos, sin, cache_layer.keys, cache_layer.values,
+                                                         cache_length, scratch.query_output)
+            del packed
+            key, value = cache_layer.keys, cache_layer.values
+            fused_post_qkv = True
+        else:
+            query, key, value = self.project_qkv(hidden_states)
+            if self.use_rope:
+                query, key = rope_native(query, key, cos, sin)
+            else:
+                query, key = apply_rotary_pos_emb(query, key, cos, sin)
+            if past_key_values is not None:
+                key, value = past_key_values.update(key, value, self.layer_idx)
+                cache_layer = past_key_values.layers[self.layer_idx]
+                cache_length = getattr(cache_layer, "cumulative_length", None)
+
+        if self._gqa_decode_applies(query, key, value, attention_mask, cache_length, past_key_values, kwargs):
+            if scratch is None:
+                out = gqa_decode_attention_native(query, key, value, attention_mask, self.scaling, cache_length)
+            else:
+                out = gqa_decode_attention_native_out(query, key, value, attention_mask, self.scaling, cache_length,
+                                                      scratch.attention_output, scratch.attention_workspace)
+            out = out.transpose(1, 2).contiguous().reshape(*input_shape, -1).contiguous()
+            if (self.use_cublaslt_projection and scratch is not None
+                    and getattr(scratch, "attention_projection_output", None) is not None):
+                return _decode_projection_out(out, self.o_proj.weight, scratch.attention_projection_output), None
+            return self.o_proj(out), None
+        if fused_post_qkv:
+            raise RuntimeError("fused packed-QKV cache update requires native GQA decode attention")
+
+        # Llama eager attention around the Flux softmax: grouped-query expansion,
+        # scaled QK, additive mask, softmax, then V.
+        key = repeat_kv(key, self.num_key_value_groups)
+        value = repeat_kv(value, self.num_key_value_groups)
+        weights = torch.matmul(query, key.transpose(2, 3))
+        if self.use_softmax and self.fuse_attention_scores and attention_mask is not None and query.shape[-2] > 1:
+            weights = attention_score_softmax_native(weights, attention_mask, self.scaling)
+        elif self.use_softmax:
+            weights = weights * self.scaling
+            if attention_mask is not None:
+                weights = weights + attention_mask
+            weights = softmax_native(weights)
+        else:
+            weights = weights * self.scaling
+            if attention_mask is not None:
+                weights = weights + attention_mask
+            weights = F.softmax(weights, dim=-1, dtype=torch.float32).to(query.dtype)
+        out = torch.matmul(weights, value)
+        out = out.transpose(1, 2).contiguous().reshape(*input_shape, -1).contiguous()
         return self.o_proj(out), weights
 
 
@@ -250,6 +401,32 @@ class FluxLlamaDecoderLayer(LlamaDecoderLayer):
         self.post_attention_layernorm = (FluxRMSNorm(source.post_attention_layernorm)
                                          if use_rmsnorm else source.post_attention_layernorm)
         self.use_residual_rmsnorm = use_residual_rmsnorm
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                position_ids: torch.LongTensor | None = None, past_key_values: Any | None = None,
+                use_cache: bool | None = False,
+                position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
+                **kwargs: Any) -> torch.Tensor:
+        """Llama layer with the post-attention add fused into residual RMSNorm (reference :740-787)."""
+        residual = hidden_states
+        hidden_states = self.input_layernorm(hidden_states)
+        attention_output, _ = self.self_attn(hidden_states=hidden_states, attention_mask=attention_mask,
+                                             position_ids=position_ids, past_key_values=past_key_values,
+                                             use_cache=use_cache, position_embeddings=position_embeddings, **kwargs)
+        if self.use_residual_rmsnorm:
+            scratch = getattr(self, "_flux_decode_scratch", None)
+            weight = self.post_attention_layernorm.weight
+            eps = self.post_attention_layernorm.variance_epsilon
+            if scratch is None:
+                hidden_states, residual = residual_rmsnorm_native(attention_output, residual, weight, eps)
+            else:
+                hidden_states, residual = residual_rmsnorm_native_out(attention_output, residual, weight, eps,
+                                                                      scratch.norm_output, scratch.residual_output)
+        else:
+            residual = residual + attention_output
+            hidden_states = self.post_attention_layernorm(residual)
+        hidden_states = self.mlp(hidden_states)
+        return residual + hidden_states
 
 
 def _check_model(model: nn.Module) -> LlamaForCausalLM:

@@ -182,12 +182,12 @@ void flux_prefill_destroy(flux_prefill* runtime);
 /* ------------------------------------------------------------------------ */
 /* Per-kernel launchers (isolated kernels of the token loop). */
 
-/* rows x cols RMSNorm: out = w * (x * rsqrt(mean(x^2) + eps)).
+/* rows x cols RMSNorm: out = w * (x * rsqrt(mean(x^2) + eps)), eps > 0 and finite, cols <= 65536.
  * Replaces rmsnorm_cuda_fp32 (csrc/rmsnorm/rmsnorm_cuda.h:9-19). */
 int flux_rmsnorm_f32(const float* x, const float* weight, float* out, int64_t rows, int64_t cols, float eps,
                      hipStream_t stream);
 
-/* residual_out = hidden + residual; norm_out = rmsnorm(residual_out).
+/* residual_out = hidden + residual; norm_out = rmsnorm(residual_out); eps >= 0 and finite.
  * Replaces residual_rmsnorm_cuda_fp32 (csrc/residual_rmsnorm/residual_rmsnorm_cuda.cu:108-150). */
 int flux_residual_rmsnorm_f32(const float* hidden, const float* residual, const float* weight, float* norm_out,
                               float* residual_out, int64_t rows, int64_t cols, float eps, hipStream_t stream);
@@ -274,6 +274,65 @@ int flux_prefill_attention_f32(const float* q, const float* key_cache, const flo
  * Replaces embedding_gather_fp32_kernel (native_prefill_runtime_cuda.cu:85-103). */
 int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq, float* hidden,
                               hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Eager operator kernels behind torch.ops.flux.* (general shapes; element
+ * strides are int64 arrays in tensor dimension order, all non-negative). */
+
+/* HF RoPE of query [B,Hq,S,D] and key [B,Hk,S,D] (strided) with cos/sin
+ * [rope_batch,S,D] (rope_batch 1 or B) into contiguous outputs; the two products
+ * are rounded separately before the add.  Replaces rope_cuda_fp32
+ * (csrc/rope/rope_cuda.cu:89-130; op schema csrc/rope/rope_torch.cpp:133-136). */
+int flux_rope_f32(const float* query, const float* key, const float* cos, const float* sin, float* query_out,
+                  float* key_out, int64_t batch, int64_t query_heads, int64_t key_heads, int64_t seq,
+                  int64_t head_dim, int64_t rope_batch, const int64_t* query_strides, const int64_t* key_strides,
+                  const int64_t* cos_strides, const int64_t* sin_strides, hipStream_t stream);
+
+/* Softmax over each contiguous row of `width` values.
+ * Replaces softmax_cuda_fp32 (csrc/softmax/softmax_cuda.cu:353-365). */
+int flux_softmax_f32(const float* input, float* output, int64_t rows, int64_t width, hipStream_t stream);
+
+/* softmax(fl(scores * scale) + mask) over contiguous scores [B,H,Q,K]; the mask
+ * has sizes 1 or the scores' size per dimension and any non-negative strides.
+ * Replaces attention_score_softmax_cuda_fp32 (csrc/softmax/softmax_cuda.cu:367-412). */
+int flux_attention_score_softmax_f32(const float* scores, const float* mask, float* output, float scale,
+                                     int64_t batch, int64_t heads, int64_t query_length, int64_t key_length,
+                                     const int64_t* mask_sizes, const int64_t* mask_strides, hipStream_t stream);
+
+/* out[r, i] = silu(packed[r, i]) * packed[r, I + i] for contiguous packed [rows, 2I].
+ * Replaces packed_swiglu_cuda_fp32 (csrc/packed_swiglu/packed_swiglu_cuda.cu:35-56). */
+int flux_packed_swiglu_f32(const float* packed, float* output, int64_t rows, int64_t intermediate,
+                           hipStream_t stream);
+
+/* One-token packed QKV [960] -> RoPE(q) into query_out [9,64]; RoPE(k) and v
+ * written to row *position of key/value caches [1,3,capacity,64]; nothing is
+ * written when *position is outside [0, capacity).  When cache_length is
+ * non-NULL it receives *position + 1 (it may alias position).
+ * Replaces packed_qkv_rope_cache_cuda_fp32 and
+ * packed_qkv_rope_cache_at_position_cuda_fp32
+ * (csrc/packed_qkv_rope_cache/packed_qkv_rope_cache_cuda.cu:125-179). */
+int flux_packed_qkv_rope_cache_f32(const float* packed_qkv, const float* cos, const float* sin, float* key_cache,
+                                   float* value_cache, const int64_t* position, int64_t* cache_length,
+                                   float* query_out, int64_t capacity, int64_t packed_stride, int64_t cos_stride,
+                                   int64_t sin_stride, const int64_t* key_strides, const int64_t* value_strides,
+                                   hipStream_t stream);
+
+/* One-token GQA attention of query [1,Hq,1,D] over strided caches [1,Hkv,capacity,D]
+ * for the first clamp(*cache_length, 1, capacity) positions (all when
+ * cache_length is NULL), with an optional additive mask broadcast from
+ * [1|1, 1|Hq, 1, 1|capacity]; output [1,Hq,1,D] contiguous.  Split-key partials
+ * go to `workspace` (size from the _workspace_bytes query; 0 for capacity <= 256).
+ * Replaces gqa_decode_attention_cuda_fp32
+ * (csrc/gqa_decode_attention/gqa_decode_attention_cuda.cu:551-633). */
+int flux_gqa_decode_attention_strided_workspace_bytes(int64_t query_heads, int64_t capacity, int64_t head_dim,
+                                                      int64_t* bytes);
+int flux_gqa_decode_attention_strided_f32(const float* query, const float* key_cache, const float* value_cache,
+                                          const float* mask, const int64_t* cache_length, float* output,
+                                          void* workspace, int64_t workspace_bytes, float scale, int64_t query_heads,
+                                          int64_t kv_heads, int64_t capacity, int64_t head_dim,
+                                          const int64_t* query_strides, const int64_t* key_strides,
+                                          const int64_t* value_strides, const int64_t* mask_sizes,
+                                          const int64_t* mask_strides, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,9 @@ against (double-precision host references in ``csrc/tests/*.cu``):
 * ``gate_up_swiglu``     -- ``csrc/packed_gate_up_gemv/packed_gate_up_gemv_cuda.cu:25-48``
 * ``greedy_argmax``      -- ``csrc/greedy_generation/greedy_generation_cuda.cu:20-95``
 * ``causal_attention``   -- ``csrc/tests/test_streaming_prefill_gqa.cu:192-260``
+* ``softmax_rows``       -- ``csrc/softmax/softmax.cpp:9-52`` (max-shifted exp, normalised)
+* ``attention_score_softmax`` -- ``csrc/attention_score_softmax/attention_score_softmax.cpp:11-80``
+* ``packed_swiglu``      -- ``csrc/packed_swiglu/packed_swiglu.cpp`` / ``flux/ops/packed_swiglu.py``
 """
 
 from __future__ import annotations
@@ -64,9 +67,11 @@ def qkv_rope_cache(hidden: torch.Tensor, norm_weight: torch.Tensor, eps: float, 
 
 
 def gqa_decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, length: int,
-                         scale: float) -> torch.Tensor:
+                         scale: float, mask: torch.Tensor | None = None) -> torch.Tensor:
     """One-token GQA. q [Hq, D]; keys/values [Hkv, >=length, D]; returns [Hq, D] float64.
 
+    ``mask`` (optional) is the additive mask already broadcast to [Hq, >=length];
+    it is added after the scale, as in ``flux/ops/gqa_decode_attention.py:74-79``.
     Written as the per-head loop of the reference's host reference
     (``csrc/tests/test_decode_ops.cu:158-195``).
     """
@@ -79,10 +84,32 @@ def gqa_decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tens
         k = keys[g, :length].double()
         v = values[g, :length].double()
         s = (k @ q[h].double()) * scale
+        if mask is not None:
+            s = s + mask[h, :length].double()
         s = s - s.max()
         p = torch.exp(s)
         out[h] = (p @ v) / p.sum()
     return out
+
+
+def softmax_rows(x: torch.Tensor) -> torch.Tensor:
+    """Softmax over the last dimension in float64: exp(x - max) / sum."""
+    x64 = x.double()
+    e = torch.exp(x64 - x64.max(dim=-1, keepdim=True).values)
+    return e / e.sum(dim=-1, keepdim=True)
+
+
+def attention_score_softmax(scores: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
+    """softmax(scores * scale + mask) over [B, H, Q, K] with the mask broadcast, float64."""
+    return softmax_rows(scores.double() * scale + mask.double())
+
+
+def packed_swiglu(packed: torch.Tensor) -> torch.Tensor:
+    """``silu(packed[..., :I]) * packed[..., I:]`` in float64."""
+    p = packed.double()
+    inter = p.shape[-1] // 2
+    gate, up = p[..., :inter], p[..., inter:]
+    return gate * torch.sigmoid(gate) * up
 
 
 def gate_up_swiglu(x: torch.Tensor, packed_gate_up: torch.Tensor) -> torch.Tensor:

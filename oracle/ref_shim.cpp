@@ -6,11 +6,15 @@
 //   /root/reference/csrc/residual_rmsnorm/residual_rmsnorm.cpp
 //   /root/reference/csrc/packed_swiglu/packed_swiglu.cpp
 //   /root/reference/csrc/rope/rope.cpp
+//   /root/reference/csrc/softmax/softmax.cpp
+//   /root/reference/csrc/attention_score_softmax/attention_score_softmax.cpp
 // by oracle/Makefile into oracle/_ref/libfluxref.so.
+#include "attention_score_softmax.h"
 #include "packed_swiglu.h"
 #include "residual_rmsnorm.h"
 #include "rmsnorm.h"
 #include "rope.h"
+#include "softmax.h"
 
 #include <exception>
 
@@ -52,6 +56,27 @@ int ref_rope(const float* q, const float* k, const float* cos, const float* sin,
         const flux::RopeStrides ks{k_heads * seq * dim, seq * dim, dim, 1};
         const flux::RopeEmbeddingStrides es{seq * dim, dim, 1};
         flux::rope_fp32(q, k, cos, sin, q_out, k_out, 1, q_heads, k_heads, seq, dim, 1, qs, ks, es, es);
+        return 0;
+    } catch (const std::exception&) {
+        return 1;
+    }
+}
+
+int ref_softmax(const float* input, float* output, long rows, long width) {
+    try {
+        flux::softmax_fp32(input, output, rows, width);
+        return 0;
+    } catch (const std::exception&) {
+        return 1;
+    }
+}
+
+// Contiguous scores [B, H, Q, K]; contiguous mask [mb, mh, mq, mk] (each 1 or full).
+int ref_attention_score_softmax(const float* scores, const float* mask, float* output, float scale, long batch,
+                                long heads, long query_length, long key_length, long mb, long mh, long mq, long mk) {
+    try {
+        flux::attention_score_softmax_fp32(scores, mask, output, scale, batch, heads, query_length, key_length, mb,
+                                           mh, mq, mk);
         return 0;
     } catch (const std::exception&) {
         return 1;

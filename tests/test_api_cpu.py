@@ -1,6 +1,7 @@
 """Python surface checks on the CPU (no GPU): enable_flux_ops wiring, packed
-parameters, state-dict transparency, eager equivalence, and the runtime's
-input validation that happens before the native boundary.
+parameters, state-dict transparency, the GPU-only contract of the enabled
+model, and the runtime's input validation that happens before the native
+boundary.
 
 Mirrors tests/test_system.py:136-292 of the reference (module replacement and
 HF equivalence on a small model, state-dict round trip, error contract)."""
@@ -83,14 +84,11 @@ def test_packed_parameters_and_equivalence():
         mlp = ref_layer.mlp
         assert torch.equal(layer.mlp.gate_up_proj.weight, torch.cat((mlp.gate_proj.weight, mlp.up_proj.weight)))
     assert flux._flux_operator_categories == tuple(sorted(smollm2_flux.FINAL_FLUX_OPERATOR_CATEGORIES))
+    # The Flux operators have no CPU kernel: an enabled model computes on GPU
+    # tensors only (the HF-equivalence check is tests/test_ops_gpu.py).
     ids = (torch.arange(9).unsqueeze(0) * 11 + 3) % 128
-    with torch.inference_mode():
-        a = reference(input_ids=ids).logits
-        b = flux(input_ids=ids).logits
-        torch.testing.assert_close(b, a, rtol=2e-4, atol=2e-5)
-        generated_ref = reference.generate(input_ids=ids, do_sample=False, max_new_tokens=5, pad_token_id=0)
-        generated = flux.generate(input_ids=ids, do_sample=False, max_new_tokens=5, pad_token_id=0)
-    assert torch.equal(generated, generated_ref)
+    with torch.inference_mode(), pytest.raises(RuntimeError, match="no CPU kernel"):
+        flux(input_ids=ids)
 
 
 def test_state_dict_keeps_hf_keys_and_round_trips(tmp_path):

@@ -12,6 +12,7 @@ from __future__ import annotations
 import ctypes
 import hashlib
 import json
+import math
 import os
 
 import numpy as np
@@ -149,6 +150,33 @@ def test_gqa_decode_closed_forms():
     vv = v.repeat_interleave(3, dim=0).double()
     p = torch.softmax((kk @ q.double()[:, :, None])[..., 0] * 0.125, dim=-1)
     torch.testing.assert_close(out, (p[:, None, :] @ vv)[:, 0])
+    # Additive mask: a constant shift changes nothing; -inf everywhere but one
+    # position selects that position's V row; a per-head mask indexes heads.
+    torch.testing.assert_close(ref.gqa_decode_attention(q, k, v, 40, 0.125, torch.full((9, 40), 7.5)), out)
+    only = torch.full((9, 40), float("-inf"))
+    only[:, 17] = 0.0
+    torch.testing.assert_close(ref.gqa_decode_attention(q, k, v, 40, 0.125, only),
+                               v[:, 17].double().repeat_interleave(3, dim=0))
+    per_head = torch.full((9, 40), float("-inf"))
+    per_head[torch.arange(9), torch.arange(9) * 4] = 0.0
+    torch.testing.assert_close(ref.gqa_decode_attention(q, k, v, 40, 0.125, per_head),
+                               torch.stack([v[h // 3, 4 * h].double() for h in range(9)]))
+
+
+def test_softmax_and_swiglu_closed_forms():
+    torch.testing.assert_close(ref.softmax_rows(torch.zeros(3, 8)), torch.full((3, 8), 0.125, dtype=torch.float64))
+    x = torch.randn(4, 33, generator=torch.Generator().manual_seed(5))
+    torch.testing.assert_close(ref.softmax_rows(x.double() + 100.0), ref.softmax_rows(x))
+    torch.testing.assert_close(ref.softmax_rows(x).sum(-1), torch.ones(4, dtype=torch.float64))
+    one_hot = torch.tensor([[0.0, float("-inf"), float("-inf")]])
+    assert torch.equal(ref.softmax_rows(one_hot), torch.tensor([[1.0, 0.0, 0.0]], dtype=torch.float64))
+    scores = torch.randn(1, 2, 3, 4, generator=torch.Generator().manual_seed(6))
+    mask = torch.tensor([0.0, 0.0, float("-inf"), float("-inf")]).view(1, 1, 1, 4)
+    out = ref.attention_score_softmax(scores, mask, 0.5)
+    assert torch.all(out[..., 2:] == 0)
+    torch.testing.assert_close(out[..., :2], ref.softmax_rows(scores[..., :2] * 0.5))
+    torch.testing.assert_close(ref.packed_swiglu(torch.tensor([[0.0, 2.0, 5.0, 7.0]])),
+                               torch.tensor([[0.0, 2.0 / (1.0 + math.exp(-2.0)) * 7.0]], dtype=torch.float64))
 
 
 def test_causal_attention_closed_forms():
@@ -209,8 +237,23 @@ def test_oracle_against_reference_cpu_sources():
     packed = torch.randn(3, 2 * 1536, generator=g)
     sw = torch.empty(3, 1536)
     assert lib.ref_packed_swiglu(p(packed), p(sw), 3, 1536) == 0
-    gg, uu = packed[:, :1536].double(), packed[:, 1536:].double()
-    torch.testing.assert_close(sw.double(), gg * torch.sigmoid(gg) * uu, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(sw.double(), ref.packed_swiglu(packed), rtol=1e-5, atol=1e-6)
+    # Softmax and the scaled + broadcast-masked attention-score softmax.
+    lib.ref_softmax.argtypes = [fp, fp, L, L]
+    lib.ref_attention_score_softmax.argtypes = [fp, fp, fp, F, L, L, L, L, L, L, L, L]
+    for width in (1, 17, 129, 1000):
+        x = 3.0 * torch.randn(5, width, generator=g)
+        sm = torch.empty_like(x)
+        assert lib.ref_softmax(p(x), p(sm), 5, width) == 0
+        torch.testing.assert_close(sm.double(), ref.softmax_rows(x), rtol=1e-5, atol=1e-7)
+    scores = 3.0 * torch.randn(2, 3, 5, 17, generator=g)
+    for mshape in ((2, 1, 5, 17), (1, 3, 1, 17), (1, 1, 1, 1), (2, 3, 5, 17)):
+        mask = torch.randn(mshape, generator=g)
+        out = torch.empty_like(scores)
+        assert lib.ref_attention_score_softmax(p(scores), p(mask.contiguous()), p(out), ctypes.c_float(0.25), 2, 3,
+                                               5, 17, *mshape) == 0
+        torch.testing.assert_close(out.double(), ref.attention_score_softmax(scores, mask, 0.25), rtol=1e-5,
+                                   atol=1e-7)
     # RoPE: the reference's un-fused rounding equals ours bit for bit.
     q = torch.randn(9, 5, 64, generator=g)
     k = torch.randn(3, 5, 64, generator=g)
