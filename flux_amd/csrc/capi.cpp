@@ -529,7 +529,7 @@ int flux_gqa_decode_attention_strided_f32(const float* query, const float* key_c
     args.query_heads = static_cast<int>(query_heads);
     args.groups = static_cast<int>(query_heads / kv_heads);
     args.dim = static_cast<int>(head_dim);
-    args.chunks = flux::gqa_strided_chunks(capacity);
+    args.chunks = flux::gqa_strided_chunks(capacity, head_dim);
     args.capacity = capacity;
     for (int i = 0; i < 4; ++i) {
         args.q_strides[i] = query_strides[i];
@@ -547,8 +547,9 @@ int flux_gqa_decode_attention_strided_f32(const float* query, const float* key_c
             args.mask_strides[i] = mask_sizes[i] == 1 ? 0 : mask_strides[i];
         }
     }
-    args.vec = key_strides[3] == 1 && (head_dim & 3) == 0 && (key_strides[1] & 3) == 0 && (key_strides[2] & 3) == 0 &&
-               aligned16(key_cache);
+    args.vec = key_strides[3] == 1 && value_strides[3] == 1 && (head_dim & 3) == 0 && (key_strides[1] & 3) == 0 &&
+               (key_strides[2] & 3) == 0 && (value_strides[1] & 3) == 0 && (value_strides[2] & 3) == 0 &&
+               aligned16(key_cache) && aligned16(value_cache);
     return from_hip(flux::launch_gqa_strided(args, stream), "flux_gqa_decode_attention_strided_f32");
 }
 

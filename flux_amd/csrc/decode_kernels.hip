@@ -1286,47 +1286,6 @@ __global__ void install_state_kernel(const int64_t* token_src, int64_t position_
     if (write_generated0) generated[0] = token;
 }
 
-__global__ void rmsnorm_rows_kernel(const float* x, const float* w, float* out, int64_t rows, int cols, float eps) {
-    __shared__ float red[kWavesPerWG];
-    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const float* xr = x + row * cols;
-        float ss = 0.0f;
-        for (int c = tid_opaque(); c < cols; c += blockDim.x) ss = fmaf(xr[c], xr[c], ss);
-        ss = wave_sum(ss);
-        if ((tid_opaque() & 63) == 0) red[tid_opaque() >> 6] = ss;
-        __syncthreads();
-        float total = 0.0f;
-        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += red[w];
-        const float inv = rms_inverse(total, cols, eps);
-        for (int c = tid_opaque(); c < cols; c += blockDim.x) out[row * cols + c] = w[c] * (xr[c] * inv);
-        __syncthreads();
-    }
-}
-
-__global__ void residual_rmsnorm_rows_kernel(const float* hidden, const float* residual, const float* w, float* norm_out,
-                                             float* residual_out, int64_t rows, int cols, float eps) {
-    __shared__ float red[kWavesPerWG];
-    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        float ss = 0.0f;
-        for (int c = tid_opaque(); c < cols; c += blockDim.x) {
-            const float r = hidden[row * cols + c] + residual[row * cols + c];
-            residual_out[row * cols + c] = r;
-            ss = fmaf(r, r, ss);
-        }
-        ss = wave_sum(ss);
-        if ((tid_opaque() & 63) == 0) red[tid_opaque() >> 6] = ss;
-        __syncthreads();
-        float total = 0.0f;
-        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += red[w];
-        const float inv = rms_inverse(total, cols, eps);
-        for (int c = tid_opaque(); c < cols; c += blockDim.x) {
-            const float r = hidden[row * cols + c] + residual[row * cols + c];
-            norm_out[row * cols + c] = w[c] * (r * inv);
-        }
-        __syncthreads();
-    }
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1436,21 +1395,6 @@ hipError_t launch_install_state(const int64_t* token_src, int64_t position_value
                                 int64_t* step, int64_t* generated, hipStream_t stream) {
     hipLaunchKernelGGL(install_state_kernel, dim3(1), dim3(64), 0, stream, token_src, position_value, step_value,
                        write_generated0 ? 1 : 0, input_token, position, cache_length, step, generated);
-    return hipGetLastError();
-}
-
-hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows, int cols, float eps,
-                               hipStream_t stream) {
-    const int grid = static_cast<int>(rows < 4096 ? rows : 4096);
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, x, w, out, rows, cols, eps);
-    return hipGetLastError();
-}
-
-hipError_t launch_residual_rmsnorm_rows(const float* hidden, const float* residual, const float* w, float* norm_out,
-                                        float* residual_out, int64_t rows, int cols, float eps, hipStream_t stream) {
-    const int grid = static_cast<int>(rows < 4096 ? rows : 4096);
-    hipLaunchKernelGGL(residual_rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, hidden, residual, w, norm_out,
-                       residual_out, rows, cols, eps);
     return hipGetLastError();
 }
 

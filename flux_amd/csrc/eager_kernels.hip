@@ -60,15 +60,58 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(const float* __restrict_
     }
 }
 
+// RoPE on float4 quads: thread per (row, quad); needs unit dimension strides,
+// head_dim % 8 == 0 and 16-byte aligned rows (checked by the launcher).
+__global__ void __launch_bounds__(256) rope_quads_kernel(const float* __restrict__ query,
+                                                         const float* __restrict__ key,
+                                                         const float* __restrict__ cos_table,
+                                                         const float* __restrict__ sin_table, float* query_out,
+                                                         float* key_out, RopeShape shape) {
+    const int64_t quads = shape.head_dim / 4;
+    const int64_t heads = shape.query_heads + shape.key_heads;
+    const int64_t items = shape.batch * heads * shape.seq * quads;
+    const int64_t half = shape.head_dim / 2;
+    for (int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; item < items;
+         item += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t d0 = 4 * (item % quads);
+        const int64_t row = item / quads;
+        const int64_t t = row % shape.seq;
+        const int64_t bh = row / shape.seq;
+        const int64_t head_all = bh % heads;
+        const int64_t b = bh / heads;
+        const bool is_query = head_all < shape.query_heads;
+        const int64_t head = is_query ? head_all : head_all - shape.query_heads;
+        const int64_t* st = is_query ? shape.query_strides : shape.key_strides;
+        const float* in = (is_query ? query : key) + b * st[0] + head * st[1] + t * st[2];
+        const int64_t out_heads = is_query ? shape.query_heads : shape.key_heads;
+        float* out = (is_query ? query_out : key_out) + ((b * out_heads + head) * shape.seq + t) * shape.head_dim;
+        const int64_t rb = shape.rope_batch == 1 ? 0 : b;
+        const float4 c = *reinterpret_cast<const float4*>(cos_table + rb * shape.cos_strides[0] +
+                                                          t * shape.cos_strides[1] + d0);
+        const float4 sn = *reinterpret_cast<const float4*>(sin_table + rb * shape.sin_strides[0] +
+                                                           t * shape.sin_strides[1] + d0);
+        const bool first = d0 < half;
+        const float4 x = *reinterpret_cast<const float4*>(in + d0);
+        const float4 p = *reinterpret_cast<const float4*>(in + (first ? d0 + half : d0 - half));
+        *reinterpret_cast<float4*>(out + d0) =
+            make_float4(rope_value(x.x, p.x, first, c.x, sn.x), rope_value(x.y, p.y, first, c.y, sn.y),
+                        rope_value(x.z, p.z, first, c.z, sn.z), rope_value(x.w, p.w, first, c.w, sn.w));
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Row softmax.  A "source" yields the pre-softmax value of (row, column):
 // the plain input, or fl(fl(score * scale) + mask) with a broadcast mask.
+// load4 returns columns [col, col + 4) (width % 4 == 0, 16-byte aligned rows).
 struct PlainSource {
     const float* input;
     int64_t width;
     __device__ __forceinline__ int64_t row_context(int64_t) const { return 0; }
     __device__ __forceinline__ float load(int64_t row, int64_t, int64_t col) const {
         return input[row * width + col];
+    }
+    __device__ __forceinline__ float4 load4(int64_t row, int64_t, int64_t col) const {
+        return *reinterpret_cast<const float4*>(input + row * width + col);
     }
 };
 
@@ -91,7 +134,34 @@ struct MaskedScoreSource {
         const float scaled = scores[row * width + col] * scale;
         return scaled + mask[mask_row + col * mask_strides[3]];
     }
+    // The mask quad is one float4 when its key stride is 1 and the row start is
+    // 16-byte aligned, one broadcast value when the key dimension is broadcast,
+    // else four strided loads (e.g. HF's causal mask sliced from a wider one).
+    __device__ __forceinline__ float4 load4(int64_t row, int64_t mask_row, int64_t col) const {
+#pragma clang fp contract(off)
+        const float4 sv = *reinterpret_cast<const float4*>(scores + row * width + col);
+        float4 mv;
+        const int64_t ks = mask_strides[3];
+        if (ks == 0) {
+            const float m = mask[mask_row];
+            mv = make_float4(m, m, m, m);
+        } else if (ks == 1 && ((reinterpret_cast<uintptr_t>(mask + mask_row) & 15) == 0)) {
+            mv = *reinterpret_cast<const float4*>(mask + mask_row + col);
+        } else {
+            const float* m = mask + mask_row + col * ks;
+            mv = make_float4(m[0], m[ks], m[2 * ks], m[3 * ks]);
+        }
+        return make_float4(sv.x * scale + mv.x, sv.y * scale + mv.y, sv.z * scale + mv.z, sv.w * scale + mv.w);
+    }
 };
+
+__device__ __forceinline__ float max4(float4 v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+
+__device__ __forceinline__ float4 exp4_shift(float4 v, float m) {
+    return make_float4(expf(v.x - m), expf(v.y - m), expf(v.z - m), expf(v.w - m));
+}
+
+__device__ __forceinline__ float4 div4(float4 v, float d) { return make_float4(v.x / d, v.y / d, v.z / d, v.w / d); }
 
 // One wave per row; kItems values per lane stay in registers (width <= 64*kItems).
 template <int kItems, class Source>
@@ -207,11 +277,71 @@ int grid_for(int64_t units, int64_t per_block) {
     return static_cast<int>(blocks < (int64_t{1} << 20) ? blocks : (int64_t{1} << 20));
 }
 
+// float4 form: one wave per row, kQuads float4 per lane (width <= 256 kQuads);
+// the row stays in registers up to width 8192.
+template <int kQuads, class Source>
+__global__ void __launch_bounds__(256) softmax_wave4_kernel(Source src, float* out, int64_t rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t width = src.width;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < rows;
+         row += static_cast<int64_t>(gridDim.x) * 4) {
+        const int64_t ctx = src.row_context(row);
+        float4 v[kQuads];
+        float mx = -FLT_MAX;
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int64_t col = 4 * (lane + 64 * j);
+            if (col < width) {
+                v[j] = src.load4(row, ctx, col);
+                mx = fmaxf(mx, max4(v[j]));
+            }
+        }
+        mx = wave_max(mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int64_t col = 4 * (lane + 64 * j);
+            if (col < width) {
+                v[j] = exp4_shift(v[j], mx);
+                sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+            }
+        }
+        sum = wave_sum(sum);
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int64_t col = 4 * (lane + 64 * j);
+            if (col < width) *reinterpret_cast<float4*>(out + row * width + col) = div4(v[j], sum);
+        }
+    }
+}
+
 template <class Source>
-hipError_t launch_softmax_rows(const Source& src, float* out, int64_t rows, hipStream_t stream) {
+hipError_t launch_softmax_rows(const Source& src, float* out, int64_t rows, bool vec, hipStream_t stream) {
     const int64_t width = src.width;
     const int wave_grid = grid_for(rows, 4);
     const int row_grid = grid_for(rows, 1);
+    if (vec && width <= 8192) {
+        if (width <= 256) {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<1, Source>), dim3(wave_grid), dim3(256), 0, stream,
+                               src, out, rows);
+        } else if (width <= 512) {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<2, Source>), dim3(wave_grid), dim3(256), 0, stream,
+                               src, out, rows);
+        } else if (width <= 1024) {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<4, Source>), dim3(wave_grid), dim3(256), 0, stream,
+                               src, out, rows);
+        } else if (width <= 2048) {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<8, Source>), dim3(wave_grid), dim3(256), 0, stream,
+                               src, out, rows);
+        } else if (width <= 4096) {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<16, Source>), dim3(wave_grid), dim3(256), 0,
+                               stream, src, out, rows);
+        } else {
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave4_kernel<32, Source>), dim3(wave_grid), dim3(256), 0,
+                               stream, src, out, rows);
+        }
+        return hipGetLastError();
+    }
     if (width <= 64) {
         hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_wave_kernel<1, Source>), dim3(wave_grid), dim3(256), 0, stream, src,
                            out, rows);
@@ -240,6 +370,114 @@ hipError_t launch_softmax_rows(const Source& src, float* out, int64_t rows, hipS
         hipLaunchKernelGGL(HIP_KERNEL_NAME(softmax_block_kernel<0, Source>), dim3(row_grid), dim3(kRowThreads), 0,
                            stream, src, out, rows);
     }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm rows (HF rounding: w * (x * (1 / sqrt(mean(x^2) + eps)))), and the
+// residual form that also stores r = hidden + residual and normalizes r.
+// Wave per row with the row in registers as float4 quads (cols % 4 == 0,
+// aligned rows, cols <= 4096); otherwise a block per row with scalar loads.
+template <int kQuads, bool kResidual>
+__global__ void __launch_bounds__(256) rmsnorm_wave4_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ residual,
+                                                            const float* __restrict__ w, float* norm_out,
+                                                            float* residual_out, int64_t rows, int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < rows;
+         row += static_cast<int64_t>(gridDim.x) * 4) {
+        float4 v[kQuads];
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c < cols) {
+                v[j] = *reinterpret_cast<const float4*>(x + row * cols + c);
+                if constexpr (kResidual) {
+                    const float4 r = *reinterpret_cast<const float4*>(residual + row * cols + c);
+                    v[j] = make_float4(v[j].x + r.x, v[j].y + r.y, v[j].z + r.z, v[j].w + r.w);
+                    *reinterpret_cast<float4*>(residual_out + row * cols + c) = v[j];
+                }
+                ss = fmaf(v[j].x, v[j].x, ss);
+                ss = fmaf(v[j].y, v[j].y, ss);
+                ss = fmaf(v[j].z, v[j].z, ss);
+                ss = fmaf(v[j].w, v[j].w, ss);
+            }
+        }
+        const float inv = rms_inverse(wave_sum(ss), cols, eps);
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c < cols) {
+                const float4 g = *reinterpret_cast<const float4*>(w + c);
+                *reinterpret_cast<float4*>(norm_out + row * cols + c) =
+                    make_float4(g.x * (v[j].x * inv), g.y * (v[j].y * inv), g.z * (v[j].z * inv),
+                                g.w * (v[j].w * inv));
+            }
+        }
+    }
+}
+
+template <bool kResidual>
+__global__ void __launch_bounds__(256) rmsnorm_block_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ residual,
+                                                            const float* __restrict__ w, float* norm_out,
+                                                            float* residual_out, int64_t rows, int cols, float eps) {
+    __shared__ float red[4];
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        float ss = 0.0f;
+        for (int c = threadIdx.x; c < cols; c += 256) {
+            float r = x[row * cols + c];
+            if constexpr (kResidual) r = r + residual[row * cols + c];
+            ss = fmaf(r, r, ss);
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float inv = rms_inverse((red[0] + red[1]) + (red[2] + red[3]), cols, eps);
+        // Every thread has read red[] before the next row's writes.
+        __syncthreads();
+        for (int c = threadIdx.x; c < cols; c += 256) {
+            float r = x[row * cols + c];
+            if constexpr (kResidual) {
+                r = r + residual[row * cols + c];
+                residual_out[row * cols + c] = r;
+            }
+            norm_out[row * cols + c] = w[c] * (r * inv);
+        }
+    }
+}
+
+template <bool kResidual>
+hipError_t launch_rmsnorm_any(const float* x, const float* residual, const float* w, float* norm_out,
+                              float* residual_out, int64_t rows, int cols, float eps, hipStream_t stream) {
+    auto aligned = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool quads = cols % 4 == 0 && cols <= 4096 && aligned(x) && aligned(residual) && aligned(w) &&
+                       aligned(norm_out) && aligned(residual_out);
+    if (!quads) {
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(rmsnorm_block_kernel<kResidual>), dim3(grid_for(rows, 1)), dim3(256), 0,
+                           stream, x, residual, w, norm_out, residual_out, rows, cols, eps);
+        return hipGetLastError();
+    }
+    const int needed = (cols / 4 + 63) / 64;
+    const dim3 grid(grid_for(rows, 4));
+#define FLUX_LAUNCH_RMSNORM4(Q)                                                                                   \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(rmsnorm_wave4_kernel<Q, kResidual>), grid, dim3(256), 0, stream, x, residual, \
+                       w, norm_out, residual_out, rows, cols, eps)
+    if (needed <= 1) {
+        FLUX_LAUNCH_RMSNORM4(1);
+    } else if (needed <= 2) {
+        FLUX_LAUNCH_RMSNORM4(2);
+    } else if (needed <= 3) {
+        FLUX_LAUNCH_RMSNORM4(3);
+    } else if (needed <= 4) {
+        FLUX_LAUNCH_RMSNORM4(4);
+    } else if (needed <= 8) {
+        FLUX_LAUNCH_RMSNORM4(8);
+    } else {
+        FLUX_LAUNCH_RMSNORM4(16);
+    }
+#undef FLUX_LAUNCH_RMSNORM4
     return hipGetLastError();
 }
 
@@ -304,7 +542,8 @@ __global__ void __launch_bounds__(256) packed_qkv_rope_cache_kernel(PackedQkvArg
 }
 
 // ---------------------------------------------------------------------------
-// Strided one-token GQA decode attention.  Block (query head h, key chunk c)
+// Strided one-token GQA decode attention, any head_dim (head_dim 64 has the
+// faster gqa_strided_chunk64_kernel below).  Block (query head h, key chunk c)
 // scores keys [256c, 256c+256) of KV head h / groups: 16 lanes per key (4 keys
 // per wave per step), then the chunk softmax and P.V with lanes over head_dim.
 // With one chunk the block writes the normalized output; otherwise it writes
@@ -403,18 +642,165 @@ __global__ void __launch_bounds__(256) gqa_strided_chunk_kernel(GqaStridedArgs a
     }
 }
 
-__global__ void __launch_bounds__(64) gqa_strided_merge_kernel(const float* __restrict__ workspace, float* out,
-                                                               int chunks, int dim) {
-    const int h = blockIdx.x;
-    const float* parts = workspace + static_cast<int64_t>(h) * chunks * (dim + 2);
+// head_dim 64: block (query head h, 128-key chunk).  Thread (slot = t / 16,
+// l16 = t % 16) owns keys slot + 16 i (i < 8) and dims [4 l16, 4 l16 + 4): all
+// 8 K and 8 V float4s are issued before any arithmetic, so one block waits for
+// one HBM round trip.  QK is a 16-lane row reduction per key; P.V accumulates
+// per lane and is reduced over the 16 slots (xor-16/32 shuffles, then LDS).
+constexpr int kGqa64Keys = 8;
+constexpr int kGqa64Chunk = 16 * kGqa64Keys;  // 128
+
+template <bool kVec>
+__device__ __forceinline__ float4 load_row4(const float* row, int64_t dim_stride, int d0) {
+    if constexpr (kVec) {
+        return *reinterpret_cast<const float4*>(row + d0);
+    } else {
+        return make_float4(row[d0 * dim_stride], row[(d0 + 1) * dim_stride], row[(d0 + 2) * dim_stride],
+                           row[(d0 + 3) * dim_stride]);
+    }
+}
+
+template <bool kVec>
+__global__ void __launch_bounds__(256) gqa_strided_chunk64_kernel(GqaStridedArgs a) {
+    __shared__ float red[4 * 64];
+    __shared__ float stat[8];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int slot = t >> 4;
+    const int d0 = 4 * (t & 15);
+    const int h = blockIdx.x / a.chunks;
+    const int c = blockIdx.x % a.chunks;
+    const int kh = h / a.groups;
+    int64_t valid = a.cache_length != nullptr ? *a.cache_length : a.capacity;
+    valid = valid < 1 ? 1 : (valid > a.capacity ? a.capacity : valid);
+    const int64_t begin = static_cast<int64_t>(c) * kGqa64Chunk;
+    const int64_t left = valid - begin;
+    const int n = left <= 0 ? 0 : (left >= kGqa64Chunk ? kGqa64Chunk : static_cast<int>(left));
+
+    const float* kbase = a.k + kh * a.k_strides[1] + begin * a.k_strides[2];
+    const float* vbase = a.v + kh * a.v_strides[1] + begin * a.v_strides[2];
+    float4 kv[kGqa64Keys], vv[kGqa64Keys];
+#pragma unroll
+    for (int i = 0; i < kGqa64Keys; ++i) {
+        const int j = slot + 16 * i;
+        if (j < n) {
+            kv[i] = load_row4<kVec>(kbase + j * a.k_strides[2], a.k_strides[3], d0);
+            vv[i] = load_row4<kVec>(vbase + j * a.v_strides[2], a.v_strides[3], d0);
+        } else {
+            kv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vv[i] = kv[i];
+        }
+    }
+    const float* qrow = a.q + h * a.q_strides[1];
+    const float4 q4 = make_float4(qrow[d0 * a.q_strides[3]], qrow[(d0 + 1) * a.q_strides[3]],
+                                  qrow[(d0 + 2) * a.q_strides[3]], qrow[(d0 + 3) * a.q_strides[3]]);
+
+    float score[kGqa64Keys];
     float mx = -FLT_MAX;
-    for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, parts[c * (dim + 2) + dim]);
-    float total = 0.0f;
-    for (int c = 0; c < chunks; ++c) total += parts[c * (dim + 2) + dim + 1] * expf(parts[c * (dim + 2) + dim] - mx);
-    for (int d = threadIdx.x; d < dim; d += 64) {
+#pragma unroll
+    for (int i = 0; i < kGqa64Keys; ++i) {
+        float dot = q4.x * kv[i].x;
+        dot = fmaf(q4.y, kv[i].y, dot);
+        dot = fmaf(q4.z, kv[i].z, dot);
+        dot = fmaf(q4.w, kv[i].w, dot);
+        dot = row16_sum(dot);
+        const int j = slot + 16 * i;
+        float sc = -FLT_MAX;
+        if (j < n) {
+#pragma clang fp contract(off)
+            sc = dot * a.scale;
+            if (a.mask != nullptr) sc = sc + a.mask[h * a.mask_strides[1] + (begin + j) * a.mask_strides[3]];
+        }
+        score[i] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) stat[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(stat[0], stat[1]), fmaxf(stat[2], stat[3]));
+
+    float l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < kGqa64Keys; ++i) {
+        const int j = slot + 16 * i;
+        const float e = j < n ? expf(score[i] - mx) : 0.0f;
+        l += e;
+        acc.x = fmaf(e, vv[i].x, acc.x);
+        acc.y = fmaf(e, vv[i].y, acc.y);
+        acc.z = fmaf(e, vv[i].z, acc.z);
+        acc.w = fmaf(e, vv[i].w, acc.w);
+    }
+    // Sum over the 4 slots of this wave (rows of 16 lanes), then over the 4 waves.
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+    acc.x += __shfl_xor(acc.x, 16, kWave);
+    acc.y += __shfl_xor(acc.y, 16, kWave);
+    acc.z += __shfl_xor(acc.z, 16, kWave);
+    acc.w += __shfl_xor(acc.w, 16, kWave);
+    acc.x += __shfl_xor(acc.x, 32, kWave);
+    acc.y += __shfl_xor(acc.y, 32, kWave);
+    acc.z += __shfl_xor(acc.z, 32, kWave);
+    acc.w += __shfl_xor(acc.w, 32, kWave);
+    if (lane < 16) *reinterpret_cast<float4*>(red + wave * 64 + d0) = acc;
+    if (lane == 0) stat[4 + wave] = l;
+    __syncthreads();
+    if (t < 64) {
+        const float o = (red[t] + red[64 + t]) + (red[128 + t] + red[192 + t]);
+        const float total = (stat[4] + stat[5]) + (stat[6] + stat[7]);
+        if (a.chunks == 1) {
+            a.out[h * 64 + t] = o / total;
+        } else {
+            float* part = a.workspace + (static_cast<int64_t>(h) * a.chunks + c) * 66;
+            part[t] = o;
+            if (t == 0) {
+                part[64] = mx;
+                part[65] = total;
+            }
+        }
+    }
+}
+
+// Merge of the (o, m, l) chunk partials of one query head: chunk weights
+// exp(m_c - M) are computed once (threads over chunks) and kept in LDS; then
+// wave w sums chunks c = w mod 4 for 64 dims at a time and LDS adds the 4 waves.
+constexpr int kGqaMaxChunks = 256;
+
+__global__ void __launch_bounds__(256) gqa_strided_merge_kernel(const float* __restrict__ workspace, float* out,
+                                                                int chunks, int dim) {
+    __shared__ float weight[kGqaMaxChunks];
+    __shared__ float red[4 * 64];
+    __shared__ float stat[8];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int h = blockIdx.x;
+    const int64_t stride = dim + 2;
+    const float* parts = workspace + static_cast<int64_t>(h) * chunks * stride;
+    const float m = t < chunks ? parts[t * stride + dim] : -FLT_MAX;
+    const float l = t < chunks ? parts[t * stride + dim + 1] : 0.0f;
+    float mx = wave_max(m);
+    if (lane == 0) stat[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(stat[0], stat[1]), fmaxf(stat[2], stat[3]));
+    const float w = t < chunks ? expf(m - mx) : 0.0f;
+    if (t < chunks) weight[t] = w;
+    float total = wave_sum(l * w);
+    if (lane == 0) stat[4 + wave] = total;
+    __syncthreads();
+    total = (stat[4] + stat[5]) + (stat[6] + stat[7]);
+    for (int d0 = 0; d0 < dim; d0 += 64) {
+        const int d = d0 + lane;
         float o = 0.0f;
-        for (int c = 0; c < chunks; ++c) o += parts[c * (dim + 2) + d] * expf(parts[c * (dim + 2) + dim] - mx);
-        out[h * dim + d] = o / total;
+        if (d < dim) {
+#pragma unroll 4
+            for (int c = wave; c < chunks; c += 4) o = fmaf(parts[c * stride + d], weight[c], o);
+        }
+        red[wave * 64 + lane] = o;
+        __syncthreads();
+        if (wave == 0 && d < dim) out[h * dim + d] = ((red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane])) / total;
+        __syncthreads();
     }
 }
 
@@ -426,13 +812,40 @@ __global__ void __launch_bounds__(64) gqa_strided_merge_kernel(const float* __re
 hipError_t launch_rope(const float* query, const float* key, const float* cos_table, const float* sin_table,
                        float* query_out, float* key_out, const RopeShape& shape, hipStream_t stream) {
     const int64_t rows = shape.batch * (shape.query_heads + shape.key_heads) * shape.seq;
+    auto aligned = [](const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    bool quads = shape.head_dim % 8 == 0 && shape.query_strides[3] == 1 && shape.key_strides[3] == 1 &&
+                 shape.cos_strides[2] == 1 && shape.sin_strides[2] == 1 && aligned(query) && aligned(key) &&
+                 aligned(cos_table) && aligned(sin_table) && aligned(query_out) && aligned(key_out);
+    for (int i = 0; i < 3; ++i) {
+        quads = quads && shape.query_strides[i] % 4 == 0 && shape.key_strides[i] % 4 == 0;
+        if (i < 2) quads = quads && shape.cos_strides[i] % 4 == 0 && shape.sin_strides[i] % 4 == 0;
+    }
+    if (quads) {
+        hipLaunchKernelGGL(rope_quads_kernel, dim3(grid_for(rows * (shape.head_dim / 4), 256)), dim3(256), 0, stream,
+                           query, key, cos_table, sin_table, query_out, key_out, shape);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(rope_rows_kernel, dim3(grid_for(rows, 4)), dim3(256), 0, stream, query, key, cos_table,
                        sin_table, query_out, key_out, shape);
     return hipGetLastError();
 }
 
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows, int cols, float eps,
+                               hipStream_t stream) {
+    return launch_rmsnorm_any<false>(x, nullptr, w, out, nullptr, rows, cols, eps, stream);
+}
+
+hipError_t launch_residual_rmsnorm_rows(const float* hidden, const float* residual, const float* w, float* norm_out,
+                                        float* residual_out, int64_t rows, int cols, float eps, hipStream_t stream) {
+    return launch_rmsnorm_any<true>(hidden, residual, w, norm_out, residual_out, rows, cols, eps, stream);
+}
+
+static bool quad_rows(const void* a, const void* b, int64_t width) {
+    return (width & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0;
+}
+
 hipError_t launch_softmax(const float* input, float* output, int64_t rows, int64_t width, hipStream_t stream) {
-    return launch_softmax_rows(PlainSource{input, width}, output, rows, stream);
+    return launch_softmax_rows(PlainSource{input, width}, output, rows, quad_rows(input, output, width), stream);
 }
 
 hipError_t launch_attention_score_softmax(const float* scores, const float* mask, float* output, float scale,
@@ -440,7 +853,8 @@ hipError_t launch_attention_score_softmax(const float* scores, const float* mask
                                           const int64_t mask_strides[4], hipStream_t stream) {
     MaskedScoreSource src{scores, mask, scale, key_length, heads, query_length, {0, 0, 0, 0}};
     for (int i = 0; i < 4; ++i) src.mask_strides[i] = mask_strides[i];
-    return launch_softmax_rows(src, output, batch * heads * query_length, stream);
+    return launch_softmax_rows(src, output, batch * heads * query_length, quad_rows(scores, output, key_length),
+                               stream);
 }
 
 hipError_t launch_packed_swiglu(const float* packed, float* out, int64_t rows, int64_t inter, hipStream_t stream) {
@@ -456,20 +870,31 @@ hipError_t launch_packed_qkv_rope_cache(const PackedQkvArgs& args, hipStream_t s
     return hipGetLastError();
 }
 
-int gqa_strided_chunks(int64_t capacity) { return static_cast<int>((capacity + kGqaChunk - 1) / kGqaChunk); }
+int gqa_strided_chunks(int64_t capacity, int64_t head_dim) {
+    const int64_t chunk = head_dim == 64 ? kGqa64Chunk : kGqaChunk;
+    return static_cast<int>((capacity + chunk - 1) / chunk);
+}
 
 size_t gqa_strided_workspace_floats(int64_t query_heads, int64_t capacity, int64_t head_dim) {
-    const int chunks = gqa_strided_chunks(capacity);
+    const int chunks = gqa_strided_chunks(capacity, head_dim);
     if (chunks <= 1) return 0;
     return static_cast<size_t>(query_heads) * chunks * (head_dim + 2);
 }
 
 hipError_t launch_gqa_strided(const GqaStridedArgs& args, hipStream_t stream) {
-    const size_t lds = (static_cast<size_t>(args.dim) + kGqaChunk + 4 * 64 + 8) * sizeof(float);
-    hipLaunchKernelGGL(gqa_strided_chunk_kernel, dim3(args.query_heads * args.chunks), dim3(256), lds, stream, args);
+    if (args.chunks < 1 || args.chunks > kGqaMaxChunks) return hipErrorInvalidValue;
+    const dim3 grid(args.query_heads * args.chunks);
+    if (args.dim == 64 && args.vec) {
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gqa_strided_chunk64_kernel<true>), grid, dim3(256), 0, stream, args);
+    } else if (args.dim == 64) {
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gqa_strided_chunk64_kernel<false>), grid, dim3(256), 0, stream, args);
+    } else {
+        const size_t lds = (static_cast<size_t>(args.dim) + kGqaChunk + 4 * 64 + 8) * sizeof(float);
+        hipLaunchKernelGGL(gqa_strided_chunk_kernel, grid, dim3(256), lds, stream, args);
+    }
     hipError_t st = hipGetLastError();
     if (st != hipSuccess || args.chunks == 1) return st;
-    hipLaunchKernelGGL(gqa_strided_merge_kernel, dim3(args.query_heads), dim3(64), 0, stream, args.workspace, args.out,
+    hipLaunchKernelGGL(gqa_strided_merge_kernel, dim3(args.query_heads), dim3(256), 0, stream, args.workspace, args.out,
                        args.chunks, args.dim);
     return hipGetLastError();
 }

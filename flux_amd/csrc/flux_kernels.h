@@ -163,15 +163,15 @@ struct GqaStridedArgs {
     int query_heads;
     int groups;                    // Hq / Hkv
     int dim;
-    int chunks;                    // gqa_strided_chunks(capacity)
-    int vec;                       // K rows contiguous, 16-byte aligned, dim % 4 == 0
+    int chunks;                    // gqa_strided_chunks(capacity, dim)
+    int vec;                       // K and V rows contiguous, 16-byte aligned, dim % 4 == 0
     int64_t capacity;
     int64_t q_strides[4];
     int64_t k_strides[4];
     int64_t v_strides[4];
     int64_t mask_strides[4];       // 0 on broadcast dimensions
 };
-int gqa_strided_chunks(int64_t capacity);
+int gqa_strided_chunks(int64_t capacity, int64_t head_dim);  // 128-key chunks for head_dim 64, else 256
 size_t gqa_strided_workspace_floats(int64_t query_heads, int64_t capacity, int64_t head_dim);
 hipError_t launch_gqa_strided(const GqaStridedArgs& args, hipStream_t stream);
 

@@ -321,7 +321,8 @@ int flux_packed_qkv_rope_cache_f32(const float* packed_qkv, const float* cos, co
  * for the first clamp(*cache_length, 1, capacity) positions (all when
  * cache_length is NULL), with an optional additive mask broadcast from
  * [1|1, 1|Hq, 1, 1|capacity]; output [1,Hq,1,D] contiguous.  Split-key partials
- * go to `workspace` (size from the _workspace_bytes query; 0 for capacity <= 256).
+ * go to `workspace` (size from the _workspace_bytes query; 0 when one chunk covers the capacity: 128 keys
+ * for head_dim 64, 256 otherwise).
  * Replaces gqa_decode_attention_cuda_fp32
  * (csrc/gqa_decode_attention/gqa_decode_attention_cuda.cu:551-633). */
 int flux_gqa_decode_attention_strided_workspace_bytes(int64_t query_heads, int64_t capacity, int64_t head_dim,

@@ -257,3 +257,19 @@ def test_fake_tensor_contracts():
 def test_out_variant_workspace_shape_matches_reference():
     query, keys = torch.empty(1, 9, 1, 64), torch.empty(1, 3, 1024, 64)
     assert native_ops.gqa_decode_out_workspace_shape(query, keys) == (1, 9, 8, 66)
+
+
+@pytest.mark.skipif(not _native.is_available(), reason="libflux_amd.so not built")
+def test_gqa_decode_workspace_sizes():
+    # head_dim 64 splits keys in chunks of 128, other head sizes in chunks of 256; one chunk needs no workspace.
+    assert native_ops.gqa_decode_workspace_bytes(9, 128, 64) == 0
+    assert native_ops.gqa_decode_workspace_bytes(9, 129, 64) == 9 * 2 * 66 * 4
+    assert native_ops.gqa_decode_workspace_bytes(9, 8192, 64) == 9 * 64 * 66 * 4
+    assert native_ops.gqa_decode_workspace_bytes(4, 256, 8) == 0
+    assert native_ops.gqa_decode_workspace_bytes(4, 600, 8) == 4 * 3 * 10 * 4
+    # The reference's out-variant workspace [1, Hq, ceil(capacity/128), D+2] always covers it.
+    for capacity in (513, 1024, 8192, 16384):
+        shape = native_ops.gqa_decode_out_workspace_shape(torch.empty(1, 9, 1, 64), torch.empty(1, 3, capacity, 64))
+        assert math.prod(shape) * 4 >= native_ops.gqa_decode_workspace_bytes(9, capacity, 64)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        native_ops.gqa_decode_workspace_bytes(9, 16385, 64)

@@ -123,13 +123,14 @@ def test_attention_score_softmax_broadcasts(gpu_device, mask_shape):
 
 
 @pytest.mark.parametrize("seq", [9, 300, 1500, 5000])
-def test_attention_score_softmax_causal_strided_mask(gpu_device, seq):
-    """HF's eager causal mask (finfo.min above the diagonal), sliced from a wider mask."""
+@pytest.mark.parametrize("pad", [0, 7])
+def test_attention_score_softmax_causal_strided_mask(gpu_device, seq, pad):
+    """HF's eager causal mask (finfo.min above the diagonal), contiguous or sliced from a wider mask."""
     g = torch.Generator(device=gpu_device).manual_seed(seq)
     scores = torch.randn((1, 2, seq, seq), generator=g, device=gpu_device) * 4.0
-    full = torch.full((seq, seq + 7), torch.finfo(torch.float32).min, device=gpu_device).triu(1)
+    full = torch.full((seq, seq + pad), torch.finfo(torch.float32).min, device=gpu_device).triu(1)
     mask = full[None, None, :, :seq]
-    assert not mask.is_contiguous()
+    assert mask.is_contiguous() == (pad == 0)
     actual = ops.attention_score_softmax_native(scores, mask, 0.125)
     expected = ref.attention_score_softmax(scores.cpu(), mask.cpu(), 0.125)
     torch.testing.assert_close(actual.cpu().double(), expected, rtol=1e-5, atol=5e-7)
@@ -153,7 +154,7 @@ def _rope_inputs(device, dim=64, heads=(9, 3)):
     return query, key, embedding.cos().unsqueeze(0).expand(2, -1, -1), embedding.sin().unsqueeze(0).expand(2, -1, -1)
 
 
-@pytest.mark.parametrize("dim,heads", [(64, (9, 3)), (8, (4, 2)), (128, (2, 2))])
+@pytest.mark.parametrize("dim,heads", [(64, (9, 3)), (8, (4, 2)), (128, (2, 2)), (6, (2, 1))])
 def test_rope_bit_exact_vs_transformers(gpu_device, dim, heads):
     inputs = _rope_inputs(gpu_device, dim, heads)
     actual = ops.rope_native(*inputs)
@@ -166,6 +167,9 @@ def test_rope_bit_exact_vs_transformers(gpu_device, dim, heads):
     assert torch.equal(q1, actual[0]) and torch.equal(k1, actual[1])
     oracle_q = ref.rope_rows(query[0].cpu(), cos[0].cpu(), sin[0].cpu())
     assert torch.equal(actual[0][0].cpu(), oracle_q)
+    # Contiguous inputs take the float4 path when head_dim % 8 == 0; the result is the same.
+    qc, kc = ops.rope_native(query.contiguous(), key.contiguous(), cos.contiguous(), sin.contiguous())
+    assert torch.equal(qc, actual[0]) and torch.equal(kc, actual[1])
 
 
 def test_rope_opcheck(gpu_device):
