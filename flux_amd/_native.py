@@ -84,6 +84,28 @@ class PrefillBuffers(ctypes.Structure):
     ]
 
 
+class LayerWeightsStruct(ctypes.Structure):
+    _fields_ = [(name, _vp) for name in ("input_norm", "packed_qkv", "o_proj", "post_norm", "gate_up", "down")]
+
+
+class LayerDecodeBuffers(ctypes.Structure):
+    _fields_ = [
+        ("input_hidden", _vp),
+        ("output", _vp),
+        ("key_cache", _vp),
+        ("value_cache", _vp),
+        ("position", _vp),
+        ("workspace", _vp),
+        ("query", _vp),
+        ("attention", _vp),
+        ("residual", _vp),
+        ("swiglu", _vp),
+        ("attention_partials", _vp),
+        ("capacity", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
 # (name, restype, argtypes) for every exported symbol.
 _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_last_error", ctypes.c_char_p, []),
@@ -113,6 +135,16 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_prefill_decode", _vp, [_vp]),
     ("flux_prefill_get_buffers", ctypes.c_int, [_vp, ctypes.POINTER(PrefillBuffers)]),
     ("flux_prefill_destroy", None, [_vp]),
+    ("flux_layer_decode_create", ctypes.c_int,
+     [ctypes.POINTER(LayerWeightsStruct), _vp, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp, _vp, ctypes.c_int64,
+      ctypes.c_double, ctypes.c_double, _stream, ctypes.POINTER(_vp)]),
+    ("flux_layer_decode_replay", ctypes.c_int, [_vp, _vp, _stream, ctypes.POINTER(_vp)]),
+    ("flux_layer_decode_reset", ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, _stream]),
+    ("flux_layer_decode_position", ctypes.c_int, [_vp, _i64]),
+    ("flux_layer_decode_replay_count", ctypes.c_int, [_vp, _i64]),
+    ("flux_layer_decode_capacity", ctypes.c_int, [_vp, _i64]),
+    ("flux_layer_decode_get_buffers", ctypes.c_int, [_vp, ctypes.POINTER(LayerDecodeBuffers)]),
+    ("flux_layer_decode_destroy", None, [_vp]),
     ("flux_rmsnorm_f32", ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _stream]),
     ("flux_residual_rmsnorm_f32", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _stream]),

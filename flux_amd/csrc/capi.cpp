@@ -20,6 +20,10 @@ struct flux_prefill {
     flux_decode decode_handle;
 };
 
+struct flux_layer_decode {
+    flux::LayerDecodeRuntime* impl;
+};
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -64,11 +68,7 @@ int isolated_grid() {
 
 // Attention split of the isolated decode-attention launcher (independent of the
 // fused kernel): enough chunks to cover `capacity` positions.
-int isolated_chunks(int64_t capacity) {
-    int chunks = 85;
-    while (flux::gqa_decode_max_positions(chunks) < capacity) chunks *= 2;
-    return chunks;
-}
+int isolated_chunks(int64_t capacity) { return flux::isolated_attention_chunks(capacity); }
 
 }  // namespace
 
@@ -399,6 +399,68 @@ int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_
         return invalid("flux_embedding_gather_f32: invalid argument");
     return from_hip(flux::launch_embedding_gather(ids, embedding, vocab, seq, hidden, stream),
                     "flux_embedding_gather_f32");
+}
+
+// ---------------------------------------------------------------------------
+// Single-layer decode runtime.
+
+int flux_layer_decode_create(const flux_layer_weights* weights, const float* rope_cos, const float* rope_sin,
+                             int64_t capacity, int64_t position, const float* initial_hidden, const float* key_source,
+                             const float* value_source, int64_t source_length, double epsilon,
+                             double attention_scale, hipStream_t stream, flux_layer_decode** out) {
+    if (weights == nullptr || out == nullptr) return invalid("flux_layer_decode_create: null argument");
+    *out = nullptr;
+    return guarded([&] {
+        const flux::LayerWeights layer{weights->input_norm, weights->packed_qkv, weights->o_proj, weights->post_norm,
+                                       weights->gate_up,    weights->down,       static_cast<float>(epsilon),
+                                       static_cast<float>(attention_scale)};
+        auto* impl = new flux::LayerDecodeRuntime(layer, rope_cos, rope_sin, capacity, position, initial_hidden,
+                                                  key_source, value_source, source_length, stream);
+        *out = new flux_layer_decode{impl};
+    });
+}
+
+int flux_layer_decode_replay(flux_layer_decode* runtime, const float* hidden, hipStream_t stream, float** output) {
+    if (runtime == nullptr) return invalid("flux_layer_decode_replay: null runtime");
+    return guarded([&] {
+        float* result = runtime->impl->replay(hidden, stream);
+        if (output) *output = result;
+    });
+}
+
+int flux_layer_decode_reset(flux_layer_decode* runtime, const float* hidden, const float* key_source,
+                            const float* value_source, int64_t source_length, int64_t position, hipStream_t stream) {
+    if (runtime == nullptr) return invalid("flux_layer_decode_reset: null runtime");
+    return guarded([&] { runtime->impl->reset(hidden, key_source, value_source, source_length, position, stream); });
+}
+
+int flux_layer_decode_position(flux_layer_decode* runtime, int64_t* out) {
+    if (runtime == nullptr || out == nullptr) return invalid("flux_layer_decode_position: null argument");
+    return guarded([&] { *out = runtime->impl->position(); });
+}
+
+int flux_layer_decode_replay_count(const flux_layer_decode* runtime, int64_t* out) {
+    if (runtime == nullptr || out == nullptr) return invalid("flux_layer_decode_replay_count: null argument");
+    *out = runtime->impl->replay_count();
+    return FLUX_OK;
+}
+
+int flux_layer_decode_capacity(const flux_layer_decode* runtime, int64_t* out) {
+    if (runtime == nullptr || out == nullptr) return invalid("flux_layer_decode_capacity: null argument");
+    *out = runtime->impl->capacity();
+    return FLUX_OK;
+}
+
+int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_decode_buffers* out) {
+    if (runtime == nullptr || out == nullptr) return invalid("flux_layer_decode_get_buffers: null argument");
+    runtime->impl->buffers(out);
+    return FLUX_OK;
+}
+
+void flux_layer_decode_destroy(flux_layer_decode* runtime) {
+    if (runtime == nullptr) return;
+    delete runtime->impl;
+    delete runtime;
 }
 
 // ---------------------------------------------------------------------------

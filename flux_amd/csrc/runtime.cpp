@@ -64,6 +64,12 @@ int device_cu_count() {
     return cus;
 }
 
+int isolated_attention_chunks(int64_t capacity) {
+    int chunks = 85;
+    while (gqa_decode_max_positions(chunks) < capacity) chunks *= 2;
+    return chunks;
+}
+
 // ---------------------------------------------------------------------------
 // DecodeRuntime
 
@@ -552,6 +558,226 @@ void PrefillRuntime::buffers(flux_prefill_buffers* out) const {
     out->sequence_length = seq_;
     out->capacity = capacity_;
     out->workspace_bytes = static_cast<int64_t>(block_bytes_);
+}
+
+// ---------------------------------------------------------------------------
+// LayerDecodeRuntime
+
+LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* rope_cos, const float* rope_sin,
+                                       int64_t capacity, int64_t position, const float* initial_hidden,
+                                       const float* key_source, const float* value_source, int64_t source_length,
+                                       hipStream_t stream)
+    : capacity_(capacity), start_position_(position), layer_(layer), rope_cos_(rope_cos), rope_sin_(rope_sin) {
+    if (capacity < 1 || capacity > kMaxCapacity)
+        invalid("flux native decode: cache capacity must be in [1, " + std::to_string(kMaxCapacity) + "]");
+    if (position < 0 || position >= capacity)
+        invalid("flux native decode: initial position must be inside cache capacity");
+    if (!std::isfinite(layer.eps) || !(layer.eps > 0.0f))
+        invalid("flux native decode: epsilon must be positive and finite");
+    if (!std::isfinite(layer.scale)) invalid("flux native decode: attention scale must be finite FP32");
+    if (!layer.input_norm || !layer.qkv || !layer.o_proj || !layer.post_norm || !layer.gate_up || !layer.down)
+        invalid("flux native decode: every layer weight is required");
+    if (rope_cos == nullptr || rope_sin == nullptr) invalid("flux native decode: RoPE tables are required");
+    validate_state(initial_hidden, key_source, value_source, source_length, position);
+    check_hip(hipGetDevice(&device_), "hipGetDevice");
+    grid_ = device_cu_count();
+    chunks_ = isolated_attention_chunks(capacity_);
+
+    try {
+        const size_t cache_elems = static_cast<size_t>(kKVHeads) * capacity_ * kHeadDim;
+        const size_t partial_floats = static_cast<size_t>(chunks_) * kKVHeads * kGroup * (kHeadDim + 2);
+        size_t offset = 0;
+        auto take = [&](size_t bytes) {
+            const size_t at = offset;
+            offset = align_up(offset + bytes, 256);
+            return at;
+        };
+        const size_t o_hidden = take(kHidden * sizeof(float));
+        const size_t o_output = take(kHidden * sizeof(float));
+        const size_t o_key = take(cache_elems * sizeof(float));
+        const size_t o_value = take(cache_elems * sizeof(float));
+        const size_t o_position = take(sizeof(int64_t));
+        const size_t o_query = take(kQHeads * kHeadDim * sizeof(float));
+        const size_t o_attention = take(kHidden * sizeof(float));
+        const size_t o_residual = take(kHidden * sizeof(float));
+        const size_t o_swiglu = take(kInter * sizeof(float));
+        const size_t o_partials = take(partial_floats * sizeof(float));
+        block_bytes_ = offset;
+        workspace_bytes_ = offset - o_query;
+        check_hip(hipMalloc(&block_, block_bytes_), "allocating layer decode buffers");
+        char* base = static_cast<char*>(block_);
+        input_hidden_ = reinterpret_cast<float*>(base + o_hidden);
+        output_ = reinterpret_cast<float*>(base + o_output);
+        key_cache_ = reinterpret_cast<float*>(base + o_key);
+        value_cache_ = reinterpret_cast<float*>(base + o_value);
+        position_ = reinterpret_cast<int64_t*>(base + o_position);
+        workspace_ = reinterpret_cast<float*>(base + o_query);
+        query_ = reinterpret_cast<float*>(base + o_query);
+        attention_ = reinterpret_cast<float*>(base + o_attention);
+        residual_ = reinterpret_cast<float*>(base + o_residual);
+        swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
+        partials_ = reinterpret_cast<float*>(base + o_partials);
+
+        check_hip(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking), "creating capture stream");
+        check_hip(hipEventCreateWithFlags(&completion_, hipEventDisableTiming), "creating completion event");
+
+        // Warm one step (as the reference does before capture), then restore the state.
+        initialize_state(initial_hidden, key_source, value_source, source_length, position, stream, false);
+        hipEvent_t setup = nullptr;
+        check_hip(hipEventCreateWithFlags(&setup, hipEventDisableTiming), "creating setup event");
+        check_hip(hipEventRecord(setup, stream), "recording setup event");
+        check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
+        run_body(capture_stream_);
+        check_hip(hipStreamSynchronize(capture_stream_), "warming layer decode");
+        check_hip(hipEventDestroy(setup), "destroying setup event");
+        initialize_state(initial_hidden, key_source, value_source, source_length, position, capture_stream_, true);
+        check_hip(hipStreamSynchronize(capture_stream_), "initialising layer decode state");
+
+        check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
+        try {
+            run_body(capture_stream_);
+        } catch (...) {
+            hipGraph_t abandoned = nullptr;
+            (void)hipStreamEndCapture(capture_stream_, &abandoned);
+            if (abandoned) (void)hipGraphDestroy(abandoned);
+            throw;
+        }
+        check_hip(hipStreamEndCapture(capture_stream_, &graph_), "ending graph capture");
+        check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating layer graph");
+        check_hip(hipStreamSynchronize(capture_stream_), "finalising capture");
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+LayerDecodeRuntime::~LayerDecodeRuntime() { release(); }
+
+void LayerDecodeRuntime::release() noexcept {
+    int previous = -1;
+    (void)hipGetDevice(&previous);
+    (void)hipSetDevice(device_);
+    if (pending_ && completion_ != nullptr) (void)hipEventSynchronize(completion_);
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    if (completion_) (void)hipEventDestroy(completion_);
+    if (capture_stream_) {
+        (void)hipStreamSynchronize(capture_stream_);
+        (void)hipStreamDestroy(capture_stream_);
+    }
+    if (block_) (void)hipFree(block_);
+    graph_exec_ = nullptr;
+    graph_ = nullptr;
+    completion_ = nullptr;
+    capture_stream_ = nullptr;
+    block_ = nullptr;
+    if (previous >= 0 && previous != device_) (void)hipSetDevice(previous);
+}
+
+void LayerDecodeRuntime::validate_state(const float* hidden, const float* key_source, const float* value_source,
+                                        int64_t source_length, int64_t position) const {
+    if (hidden == nullptr) invalid("flux native decode: hidden state is undefined");
+    if (position < 0 || position >= capacity_)
+        invalid("flux native decode: reset position must be inside cache capacity");
+    if (position > 0 && (key_source == nullptr || value_source == nullptr || source_length < position))
+        invalid("flux native decode: initial/reset K/V must be matching contiguous float32 CUDA tensors shaped "
+                "[1, 3, sequence>=position, 64]");
+}
+
+void LayerDecodeRuntime::initialize_state(const float* hidden, const float* key_source, const float* value_source,
+                                          int64_t source_length, int64_t position, hipStream_t stream,
+                                          bool clear_output) {
+    const size_t cache_bytes = static_cast<size_t>(kKVHeads) * capacity_ * kHeadDim * sizeof(float);
+    check_hip(hipMemcpyAsync(input_hidden_, hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice, stream),
+              "initialising hidden state");
+    check_hip(hipMemsetAsync(key_cache_, 0, cache_bytes, stream), "clearing K cache");
+    check_hip(hipMemsetAsync(value_cache_, 0, cache_bytes, stream), "clearing V cache");
+    if (position > 0) {
+        const size_t row_bytes = static_cast<size_t>(position) * kHeadDim * sizeof(float);
+        const size_t src_pitch = static_cast<size_t>(source_length) * kHeadDim * sizeof(float);
+        const size_t dst_pitch = static_cast<size_t>(capacity_) * kHeadDim * sizeof(float);
+        check_hip(hipMemcpy2DAsync(key_cache_, dst_pitch, key_source, src_pitch, row_bytes, kKVHeads,
+                                   hipMemcpyDeviceToDevice, stream),
+                  "importing K cache");
+        check_hip(hipMemcpy2DAsync(value_cache_, dst_pitch, value_source, src_pitch, row_bytes, kKVHeads,
+                                   hipMemcpyDeviceToDevice, stream),
+                  "importing V cache");
+    }
+    staged_position_ = position;
+    check_hip(hipMemcpyAsync(position_, &staged_position_, sizeof(int64_t), hipMemcpyHostToDevice, stream),
+              "initialising device position");
+    if (clear_output) check_hip(hipMemsetAsync(output_, 0, kHidden * sizeof(float), stream), "clearing layer output");
+}
+
+// The step, as native_decode_runtime_cuda.cu:192-310 orders it: RMSNorm + packed QKV
+// GEMV + RoPE + cache row at *position; GQA over [0, *position]; o_proj + residual;
+// RMSNorm + gate/up GEMV + SwiGLU; down + residual; then *position += 1.
+void LayerDecodeRuntime::run_body(hipStream_t stream) {
+    check_hip(launch_qkv_rope_cache(input_hidden_, layer_.input_norm, layer_.eps, layer_.qkv, rope_cos_, rope_sin_,
+                                    position_, capacity_, key_cache_, value_cache_, query_, grid_, stream),
+              "launching QKV/RoPE/cache step");
+    check_hip(launch_gqa_decode(query_, key_cache_, value_cache_, position_, capacity_, layer_.scale, chunks_,
+                                partials_, attention_, stream),
+              "launching GQA decode attention");
+    check_hip(launch_linear576_residual(attention_, layer_.o_proj, input_hidden_, residual_, kHidden, grid_, stream),
+              "launching attention output projection");
+    check_hip(launch_gate_up_swiglu(residual_, layer_.post_norm, layer_.eps, layer_.gate_up, swiglu_, grid_, stream),
+              "launching gate/up SwiGLU");
+    check_hip(launch_down_residual(swiglu_, layer_.down, residual_, output_, grid_, stream),
+              "launching down projection");
+    check_hip(launch_advance_position(position_, stream), "advancing position");
+}
+
+float* LayerDecodeRuntime::replay(const float* hidden, hipStream_t stream) {
+    if (replay_count_ >= capacity_ - start_position_) bad_state("flux native decode: fixed-capacity state is exhausted");
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering consecutive replays");
+    if (hidden != nullptr)
+        check_hip(hipMemcpyAsync(input_hidden_, hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice, stream),
+                  "copying replay hidden state");
+    check_hip(hipGraphLaunch(graph_exec_, stream), "launching layer graph");
+    check_hip(hipEventRecord(completion_, stream), "recording replay completion");
+    pending_ = true;
+    ++replay_count_;
+    return output_;
+}
+
+void LayerDecodeRuntime::reset(const float* hidden, const float* key_source, const float* value_source,
+                               int64_t source_length, int64_t position, hipStream_t stream) {
+    validate_state(hidden, key_source, value_source, source_length, position);
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) {
+        check_hip(hipEventSynchronize(completion_), "waiting to reset runtime");
+        pending_ = false;
+    }
+    initialize_state(hidden, key_source, value_source, source_length, position, stream, true);
+    check_hip(hipStreamSynchronize(stream), "resetting runtime state");
+    start_position_ = position;
+    replay_count_ = 0;
+}
+
+int64_t LayerDecodeRuntime::position() {
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting to inspect device position");
+    int64_t result = -1;
+    check_hip(hipMemcpy(&result, position_, sizeof(result), hipMemcpyDeviceToHost), "reading device position");
+    return result;
+}
+
+void LayerDecodeRuntime::buffers(flux_layer_decode_buffers* out) const {
+    out->input_hidden = input_hidden_;
+    out->output = output_;
+    out->key_cache = key_cache_;
+    out->value_cache = value_cache_;
+    out->position = position_;
+    out->workspace = workspace_;
+    out->query = query_;
+    out->attention = attention_;
+    out->residual = residual_;
+    out->swiglu = swiglu_;
+    out->attention_partials = partials_;
+    out->capacity = capacity_;
+    out->workspace_bytes = static_cast<int64_t>(workspace_bytes_);
 }
 
 }  // namespace flux

@@ -1,6 +1,7 @@
 // C++ host runtime of the MI355X SmolLM2 token loop (HIP runtime API only).
 //
-// DecodeRuntime  <-> flux::NativeSmolLM2Decode::Impl (csrc/native_decode_runtime/native_decode_runtime_cuda.cu:740-1338)
+// DecodeRuntime      <-> flux::NativeSmolLM2Decode::Impl (csrc/native_decode_runtime/native_decode_runtime_cuda.cu:740-1338)
+// LayerDecodeRuntime <-> flux::NativeSmolLM2LayerDecode::Impl (native_decode_runtime_cuda.cu:314-738)
 // PrefillRuntime <-> flux::NativeSmolLM2Prefill::Impl (csrc/native_prefill_runtime/native_prefill_runtime_cuda.cu:353-700)
 #pragma once
 
@@ -148,6 +149,69 @@ private:
     int lm_grid_ = 0;
 };
 
+// One decoder layer's token step captured in a hipGraph: input hidden [576] ->
+// output hidden [576], with the layer's own compact cache [1, 3, capacity, 64]
+// and device position (advanced by every replay).
+class LayerDecodeRuntime {
+public:
+    LayerDecodeRuntime(const LayerWeights& layer, const float* rope_cos, const float* rope_sin, int64_t capacity,
+                       int64_t position, const float* initial_hidden, const float* key_source,
+                       const float* value_source, int64_t source_length, hipStream_t stream);
+    ~LayerDecodeRuntime();
+    LayerDecodeRuntime(const LayerDecodeRuntime&) = delete;
+    LayerDecodeRuntime& operator=(const LayerDecodeRuntime&) = delete;
+
+    float* replay(const float* hidden, hipStream_t stream);
+    void reset(const float* hidden, const float* key_source, const float* value_source, int64_t source_length,
+               int64_t position, hipStream_t stream);
+    int64_t position();
+    int64_t replay_count() const { return replay_count_; }
+    int64_t capacity() const { return capacity_; }
+    void buffers(flux_layer_decode_buffers* out) const;
+
+private:
+    void validate_state(const float* hidden, const float* key_source, const float* value_source,
+                        int64_t source_length, int64_t position) const;
+    void initialize_state(const float* hidden, const float* key_source, const float* value_source,
+                          int64_t source_length, int64_t position, hipStream_t stream, bool clear_output);
+    void run_body(hipStream_t stream);
+    void release() noexcept;
+
+    int device_ = 0;
+    int grid_ = 0;
+    int chunks_ = 0;
+    int64_t capacity_ = 0;
+    int64_t start_position_ = 0;
+    int64_t replay_count_ = 0;
+    int64_t staged_position_ = 0;
+    bool pending_ = false;
+    LayerWeights layer_{};
+    const float* rope_cos_ = nullptr;
+    const float* rope_sin_ = nullptr;
+
+    void* block_ = nullptr;
+    size_t block_bytes_ = 0;
+    size_t workspace_bytes_ = 0;
+    float* input_hidden_ = nullptr;   // [576]
+    float* output_ = nullptr;         // [576]
+    float* key_cache_ = nullptr;      // [3, capacity, 64]
+    float* value_cache_ = nullptr;
+    int64_t* position_ = nullptr;
+    float* workspace_ = nullptr;      // query | attention | residual | swiglu | attention partials
+    float* query_ = nullptr;          // [9, 64]
+    float* attention_ = nullptr;      // [576]
+    float* residual_ = nullptr;       // [576] input + o_proj(attention)
+    float* swiglu_ = nullptr;         // [1536]
+    float* partials_ = nullptr;       // split-key attention partials
+
+    hipStream_t capture_stream_ = nullptr;
+    hipEvent_t completion_ = nullptr;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t graph_exec_ = nullptr;
+};
+
 int device_cu_count();
+// Key chunks of the isolated decode attention for `capacity` positions.
+int isolated_attention_chunks(int64_t capacity);
 
 }  // namespace flux

@@ -4,6 +4,7 @@ from flux_amd.runtime.native_smollm2 import (
     NativeDecodeRuntimeMemory,
     NativePrefillRuntimeMemory,
     NativeSmolLM2Decode,
+    NativeSmolLM2LayerDecode,
     NativeSmolLM2Prefill,
     native_smollm2_greedy_generate,
     native_smollm2_prefill_is_available,
@@ -14,6 +15,7 @@ __all__ = [
     "NativeDecodeRuntimeMemory",
     "NativePrefillRuntimeMemory",
     "NativeSmolLM2Decode",
+    "NativeSmolLM2LayerDecode",
     "NativeSmolLM2Prefill",
     "native_smollm2_greedy_generate",
     "native_smollm2_prefill_is_available",

@@ -623,6 +623,183 @@ class NativeSmolLM2Decode:
         return self._handle
 
 
+def _check_layer_tensor(tensor: torch.Tensor, device: torch.device, sizes: tuple[int, ...], name: str) -> None:
+    """``check_tensor`` of native_decode_runtime_cuda.cu:53-68 (same messages)."""
+    if tensor is None:
+        raise RuntimeError(f"flux native decode: {name} is undefined")
+    if tensor.device != device:
+        raise RuntimeError(f"flux native decode: {name} must be on {device}")
+    if tensor.dtype != torch.float32:
+        raise RuntimeError(f"flux native decode: {name} has the wrong dtype")
+    if tuple(tensor.shape) != tuple(sizes):
+        raise RuntimeError(f"flux native decode: {name} has shape {list(tensor.shape)}, expected {list(sizes)}")
+    if not tensor.is_contiguous():
+        raise RuntimeError(f"flux native decode: {name} must be contiguous")
+
+
+_LAYER_ADDRESS_NAMES = ("input_hidden", "output", "key_cache", "value_cache", "device_position", "workspace", "query",
+                        "attention", "residual", "swiglu", "attention_workspace")
+
+
+class NativeSmolLM2LayerDecode:
+    """One SmolLM2 decoder layer's token step as a replayable native graph.
+
+    Mirror of ``torch.classes.flux.NativeSmolLM2LayerDecode``
+    (``csrc/native_decode_runtime/native_decode_runtime.h:13-54``, registered in
+    ``native_decode_runtime_torch.cpp:5-36``): the constructor arguments, methods
+    and validation messages are the reference's; the step runs this build's
+    decode kernels (RMSNorm + packed QKV GEMV + RoPE + cache row, GQA decode,
+    o_proj + residual, RMSNorm + gate/up SwiGLU, down + residual) and advances
+    the device position.  ``replay`` returns the stable ``[1, 1, 576]`` output.
+    """
+
+    def __init__(self, initial_hidden: torch.Tensor, input_norm_weight: torch.Tensor,
+                 packed_qkv_weight: torch.Tensor, attention_output_weight: torch.Tensor,
+                 post_attention_norm_weight: torch.Tensor, packed_gate_up_weight: torch.Tensor,
+                 down_projection_weight: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                 initial_key_cache: torch.Tensor, initial_value_cache: torch.Tensor, cache_capacity: int,
+                 initial_position: int, epsilon: float, attention_scale: float) -> None:
+        import math
+
+        device = initial_hidden.device
+        if device.type != "cuda":
+            raise RuntimeError("flux native decode: initial_hidden must be a CUDA tensor")
+        capacity = int(cache_capacity)
+        position = int(initial_position)
+        if capacity < 1 or capacity > MAX_CAPACITY:
+            raise RuntimeError(f"flux native decode: cache capacity must be in [1, {MAX_CAPACITY}]")
+        if position < 0 or position >= capacity:
+            raise RuntimeError("flux native decode: initial position must be inside cache capacity")
+        if not (math.isfinite(epsilon) and epsilon > 0.0):
+            raise RuntimeError("flux native decode: epsilon must be positive and finite")
+        if not math.isfinite(attention_scale) or abs(attention_scale) > torch.finfo(torch.float32).max:
+            raise RuntimeError("flux native decode: attention scale must be finite FP32")
+        weights = (
+            (input_norm_weight, (576,), "input_norm_weight"),
+            (packed_qkv_weight, (960, 576), "packed_qkv_weight"),
+            (attention_output_weight, (576, 576), "attention_output_weight"),
+            (post_attention_norm_weight, (576,), "post_attention_norm_weight"),
+            (packed_gate_up_weight, (3072, 576), "packed_gate_up_weight"),
+            (down_projection_weight, (576, 1536), "down_projection_weight"),
+            (rope_cos, (capacity, 64), "rope_cos"),
+            (rope_sin, (capacity, 64), "rope_sin"),
+        )
+        for tensor, sizes, name in weights:
+            _check_layer_tensor(tensor, device, sizes, name)
+        self._device = device
+        self._capacity = capacity
+        self._validate_state(initial_hidden, initial_key_cache, initial_value_cache, position)
+        if not _native.is_available():
+            raise RuntimeError("Flux native layer decode runtime is not built. Run `python -m flux_amd.build`.")
+        lw = _native.LayerWeightsStruct(*[_native.ptr(t) for t, _, _ in weights[:6]])
+        raw = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            _native.check(_native.load().flux_layer_decode_create(
+                ctypes.byref(lw), _native.ptr(rope_cos), _native.ptr(rope_sin), capacity, position,
+                _native.ptr(initial_hidden), _native.ptr(initial_key_cache), _native.ptr(initial_value_cache),
+                int(initial_key_cache.shape[2]), float(epsilon), float(attention_scale),
+                _native.current_stream(device), ctypes.byref(raw)))
+        self._raw = raw
+        # The runtime borrows the weights and tables: keep them alive with it.
+        self._keepalive = tuple(t for t, _, _ in weights)
+        buffers = _native.LayerDecodeBuffers()
+        _native.check(_native.load().flux_layer_decode_get_buffers(self._raw, ctypes.byref(buffers)))
+        self._buffers = buffers
+        view = lambda address, shape, dtype: _native.device_tensor(address, shape, dtype, self, device)  # noqa: E731
+        self._output = view(buffers.output, (1, 1, 576), torch.float32)
+        self._input_hidden = view(buffers.input_hidden, (1, 1, 576), torch.float32)
+        self._key_cache = view(buffers.key_cache, (1, 3, capacity, 64), torch.float32)
+        self._value_cache = view(buffers.value_cache, (1, 3, capacity, 64), torch.float32)
+        self._position = view(buffers.position, (), torch.int64)
+        self._workspace = view(buffers.workspace, (int(buffers.workspace_bytes) // 4,), torch.float32)
+
+    def _validate_state(self, hidden: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                        position: int) -> None:
+        _check_layer_tensor(hidden, self._device, (1, 1, 576), "hidden state")
+        if position < 0 or position >= self._capacity:
+            raise RuntimeError("flux native decode: reset position must be inside cache capacity")
+        ok = (key_cache is not None and value_cache is not None and key_cache.device == self._device
+              and value_cache.device == self._device and key_cache.dtype == torch.float32
+              and value_cache.dtype == torch.float32 and key_cache.is_contiguous() and value_cache.is_contiguous()
+              and key_cache.dim() == 4 and value_cache.shape == key_cache.shape and key_cache.shape[0] == 1
+              and key_cache.shape[1] == 3 and key_cache.shape[2] >= position and key_cache.shape[3] == 64)
+        if not ok:
+            raise RuntimeError("flux native decode: initial/reset K/V must be matching contiguous float32 CUDA "
+                               "tensors shaped [1, 3, sequence>=position, 64]")
+
+    def replay(self, hidden: torch.Tensor | None = None) -> torch.Tensor:
+        """Enqueue an optional hidden copy and one graph launch; returns the output buffer."""
+        if hidden is not None:
+            _check_layer_tensor(hidden, self._device, (1, 1, 576), "replay hidden state")
+        with torch.cuda.device(self._device):
+            _native.check(_native.load().flux_layer_decode_replay(
+                self._raw, _native.ptr(hidden), _native.current_stream(self._device), None))
+        return self._output
+
+    def reset(self, hidden: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, position: int) -> None:
+        """Synchronously restore hidden state, cache and position."""
+        self._validate_state(hidden, key_cache, value_cache, int(position))
+        with torch.cuda.device(self._device):
+            _native.check(_native.load().flux_layer_decode_reset(
+                self._raw, _native.ptr(hidden), _native.ptr(key_cache), _native.ptr(value_cache),
+                int(key_cache.shape[2]), int(position), _native.current_stream(self._device)))
+
+    def output(self) -> torch.Tensor:
+        return self._output
+
+    def key_cache(self) -> torch.Tensor:
+        return self._key_cache
+
+    def value_cache(self) -> torch.Tensor:
+        return self._value_cache
+
+    def device_position(self) -> torch.Tensor:
+        return self._position
+
+    def workspace(self) -> torch.Tensor:
+        return self._workspace
+
+    def addresses(self) -> list[int]:
+        b = self._buffers
+        return [int(x or 0) for x in (b.input_hidden, b.output, b.key_cache, b.value_cache, b.position, b.workspace,
+                                      b.query, b.attention, b.residual, b.swiglu, b.attention_partials)]
+
+    def stable_addresses(self) -> dict[str, int]:
+        return dict(zip(_LAYER_ADDRESS_NAMES, self.addresses(), strict=True))
+
+    def position(self) -> int:
+        out = ctypes.c_int64()
+        with torch.cuda.device(self._device):
+            _native.check(_native.load().flux_layer_decode_position(self._raw, ctypes.byref(out)))
+        return int(out.value)
+
+    def cache_length(self) -> int:
+        return self.position()
+
+    def capacity(self) -> int:
+        return self._capacity
+
+    def replay_count(self) -> int:
+        out = ctypes.c_int64()
+        _native.check(_native.load().flux_layer_decode_replay_count(self._raw, ctypes.byref(out)))
+        return int(out.value)
+
+    def workspace_bytes(self) -> int:
+        return int(self._buffers.workspace_bytes)
+
+    def close(self) -> None:
+        raw = getattr(self, "_raw", None)
+        if raw:
+            _native.load().flux_layer_decode_destroy(raw)
+        self._raw = ctypes.c_void_p(0)
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown
+            pass
+
+
 def native_smollm2_greedy_generate(model: nn.Module, input_ids: torch.Tensor, *, max_new_tokens: int) -> torch.Tensor:
     """Generate greedily with native prefill and fused native decode."""
     if max_new_tokens < 1:
@@ -636,6 +813,7 @@ __all__ = [
     "NativeDecodeRuntimeMemory",
     "NativePrefillRuntimeMemory",
     "NativeSmolLM2Decode",
+    "NativeSmolLM2LayerDecode",
     "NativeSmolLM2Prefill",
     "native_smollm2_greedy_generate",
     "native_smollm2_prefill_is_available",

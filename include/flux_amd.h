@@ -180,6 +180,60 @@ int flux_prefill_get_buffers(const flux_prefill* runtime, flux_prefill_buffers* 
 void flux_prefill_destroy(flux_prefill* runtime);
 
 /* ------------------------------------------------------------------------ */
+/* Single-layer decode runtime: replaces torch.classes.flux.NativeSmolLM2LayerDecode
+ * (csrc/native_decode_runtime/native_decode_runtime.h:13-54,
+ *  native_decode_runtime_cuda.cu:314-738,1340-1400; registered in
+ *  native_decode_runtime_torch.cpp:5-36).
+ * One decoder layer's token step (input hidden [1,1,576] -> output [1,1,576]) with
+ * its own K/V cache [1,3,capacity,64] and device position, captured in a hipGraph.
+ * key_source/value_source: [1,3,source_length,64] contiguous, source_length >= position
+ * (may be NULL when position == 0).  Each replay writes K/V row *position, attends
+ * [0, *position] and advances the position. */
+typedef struct flux_layer_weights {
+    const float* input_norm; /* [576] */
+    const float* packed_qkv; /* [960, 576] */
+    const float* o_proj;     /* [576, 576] */
+    const float* post_norm;  /* [576] */
+    const float* gate_up;    /* [3072, 576] */
+    const float* down;       /* [576, 1536] */
+} flux_layer_weights;
+
+typedef struct flux_layer_decode flux_layer_decode;
+
+/* NativeSmolLM2LayerDecode::addresses() counterparts (native_decode_runtime_cuda.cu:1388-1406). */
+typedef struct flux_layer_decode_buffers {
+    float* input_hidden;       /* [576] */
+    float* output;             /* [576] */
+    float* key_cache;          /* [1, 3, capacity, 64] */
+    float* value_cache;        /* [1, 3, capacity, 64] */
+    int64_t* position;         /* [1] */
+    void* workspace;           /* the intermediates below, one block */
+    float* query;              /* [9, 64] */
+    float* attention;          /* [576] */
+    float* residual;           /* [576] */
+    float* swiglu;             /* [1536] */
+    float* attention_partials; /* split-key partials */
+    int64_t capacity;
+    int64_t workspace_bytes;
+} flux_layer_decode_buffers;
+
+int flux_layer_decode_create(const flux_layer_weights* weights, const float* rope_cos, const float* rope_sin,
+                             int64_t capacity, int64_t position, const float* initial_hidden, const float* key_source,
+                             const float* value_source, int64_t source_length, double epsilon,
+                             double attention_scale, hipStream_t stream, flux_layer_decode** out);
+/* One step (optional hidden copy, then graph replay); returns the output buffer.
+ * (native_decode_runtime_cuda.cu:456-481) */
+int flux_layer_decode_replay(flux_layer_decode* runtime, const float* hidden, hipStream_t stream, float** output);
+/* Synchronously restore hidden, cache and position.  (native_decode_runtime_cuda.cu:483-501) */
+int flux_layer_decode_reset(flux_layer_decode* runtime, const float* hidden, const float* key_source,
+                            const float* value_source, int64_t source_length, int64_t position, hipStream_t stream);
+int flux_layer_decode_position(flux_layer_decode* runtime, int64_t* out);
+int flux_layer_decode_replay_count(const flux_layer_decode* runtime, int64_t* out);
+int flux_layer_decode_capacity(const flux_layer_decode* runtime, int64_t* out);
+int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_decode_buffers* out);
+void flux_layer_decode_destroy(flux_layer_decode* runtime);
+
+/* ------------------------------------------------------------------------ */
 /* Per-kernel launchers (isolated kernels of the token loop). */
 
 /* rows x cols RMSNorm: out = w * (x * rsqrt(mean(x^2) + eps)), eps > 0 and finite, cols <= 65536.

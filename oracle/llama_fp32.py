@@ -132,6 +132,20 @@ class OracleLlama:
         out = out.reshape(bsz, seq, -1).contiguous()
         return F.linear(out, self._w(p + "o_proj.weight"))
 
+    def decoder_layer(self, layer: int, hidden: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                      cache: OracleCache, mask: torch.Tensor | None) -> torch.Tensor:
+        """One LlamaDecoderLayer (transformers modeling_llama.py LlamaDecoderLayer.forward)."""
+        c = self.config
+        p = f"model.layers.{layer}."
+        residual = hidden
+        x = rmsnorm(hidden, self._w(p + "input_layernorm.weight"), c.eps)
+        hidden = residual + self._attention(layer, x, cos, sin, cache, mask)
+        residual = hidden
+        x = rmsnorm(hidden, self._w(p + "post_attention_layernorm.weight"), c.eps)
+        gate = F.linear(x, self._w(p + "mlp.gate_proj.weight"))
+        up = F.linear(x, self._w(p + "mlp.up_proj.weight"))
+        return residual + F.linear(F.silu(gate) * up, self._w(p + "mlp.down_proj.weight"))
+
     def forward(self, ids: torch.Tensor, cache: OracleCache, *, all_logits: bool = False) -> torch.Tensor:
         """Run ``ids`` ``[1, S]`` after ``cache``; returns logits of the last (or all) rows."""
         c = self.config
@@ -150,15 +164,7 @@ class OracleLlama:
             mask.masked_fill_(~allowed, torch.finfo(torch.float32).min)
             mask = mask[None, None]
         for layer in range(c.layers):
-            p = f"model.layers.{layer}."
-            residual = hidden
-            x = rmsnorm(hidden, self._w(p + "input_layernorm.weight"), c.eps)
-            hidden = residual + self._attention(layer, x, cos, sin, cache, mask)
-            residual = hidden
-            x = rmsnorm(hidden, self._w(p + "post_attention_layernorm.weight"), c.eps)
-            gate = F.linear(x, self._w(p + "mlp.gate_proj.weight"))
-            up = F.linear(x, self._w(p + "mlp.up_proj.weight"))
-            hidden = residual + F.linear(F.silu(gate) * up, self._w(p + "mlp.down_proj.weight"))
+            hidden = self.decoder_layer(layer, hidden, cos, sin, cache, mask)
         hidden = rmsnorm(hidden, self._w("model.norm.weight"), c.eps)
         if not all_logits:
             hidden = hidden[:, -1:, :]

@@ -146,3 +146,14 @@ def test_geometry_and_category_validation_order():
     ids = (torch.arange(3).unsqueeze(0) * 11 + 3) % 128
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         NativeSmolLM2Decode._validate_model_and_state(model, ids[:, :1], [], [], cache_position=0, cache_capacity=4)
+
+
+def test_layer_decode_requires_gpu_tensors():
+    from flux_amd.runtime import NativeSmolLM2LayerDecode
+
+    hidden = torch.zeros(1, 1, 576)
+    with pytest.raises(RuntimeError, match="initial_hidden must be a CUDA tensor"):
+        NativeSmolLM2LayerDecode(hidden, torch.ones(576), torch.zeros(960, 576), torch.zeros(576, 576),
+                                 torch.ones(576), torch.zeros(3072, 576), torch.zeros(576, 1536), torch.zeros(8, 64),
+                                 torch.zeros(8, 64), torch.zeros(1, 3, 0, 64), torch.zeros(1, 3, 0, 64), 8, 0, 1e-5,
+                                 0.125)
