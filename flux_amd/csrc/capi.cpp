@@ -401,6 +401,19 @@ int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_
                     "flux_embedding_gather_f32");
 }
 
+int flux_decode_graph_nodes(const flux_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes) {
+    if (runtime == nullptr || kernel_nodes == nullptr || total_nodes == nullptr)
+        return invalid("flux_decode_graph_nodes: null argument");
+    return guarded([&] { runtime->impl->graph_nodes(kernel_nodes, total_nodes); });
+}
+
+int flux_host_counters(int64_t* synchronizations, int64_t* allocations, int64_t* frees) {
+    if (synchronizations == nullptr || allocations == nullptr || frees == nullptr)
+        return invalid("flux_host_counters: null argument");
+    flux::host_counters(synchronizations, allocations, frees);
+    return FLUX_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Single-layer decode runtime.
 
@@ -455,6 +468,12 @@ int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_d
     if (runtime == nullptr || out == nullptr) return invalid("flux_layer_decode_get_buffers: null argument");
     runtime->impl->buffers(out);
     return FLUX_OK;
+}
+
+int flux_layer_decode_graph_nodes(const flux_layer_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes) {
+    if (runtime == nullptr || kernel_nodes == nullptr || total_nodes == nullptr)
+        return invalid("flux_layer_decode_graph_nodes: null argument");
+    return guarded([&] { runtime->impl->graph_nodes(kernel_nodes, total_nodes); });
 }
 
 void flux_layer_decode_destroy(flux_layer_decode* runtime) {

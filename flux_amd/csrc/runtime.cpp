@@ -2,6 +2,7 @@
 #include "runtime.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 
@@ -15,6 +16,49 @@ void check_hip(hipError_t status, const char* what) {
 }
 
 namespace {
+
+// Host-visible effects of the runtimes, counted for the runtime audit: every
+// device allocation and free, and every call that blocks the host on the GPU.
+std::atomic<int64_t> g_host_syncs{0};
+std::atomic<int64_t> g_device_allocs{0};
+std::atomic<int64_t> g_device_frees{0};
+
+hipError_t counted_malloc(void** ptr, size_t bytes) {
+    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(ptr, bytes);
+}
+hipError_t counted_free(void* ptr) {
+    g_device_frees.fetch_add(1, std::memory_order_relaxed);
+    return hipFree(ptr);
+}
+hipError_t counted_stream_sync(hipStream_t stream) {
+    g_host_syncs.fetch_add(1, std::memory_order_relaxed);
+    return hipStreamSynchronize(stream);
+}
+hipError_t counted_event_sync(hipEvent_t event) {
+    g_host_syncs.fetch_add(1, std::memory_order_relaxed);
+    return hipEventSynchronize(event);
+}
+hipError_t counted_memcpy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    g_host_syncs.fetch_add(1, std::memory_order_relaxed);
+    return hipMemcpy(dst, src, bytes, kind);
+}
+
+// Kernel nodes and all nodes of an instantiated step graph.
+void count_graph_nodes(hipGraph_t graph, int64_t* kernels, int64_t* total) {
+    size_t count = 0;
+    check_hip(hipGraphGetNodes(graph, nullptr, &count), "counting graph nodes");
+    std::vector<hipGraphNode_t> nodes(count);
+    if (count > 0) check_hip(hipGraphGetNodes(graph, nodes.data(), &count), "listing graph nodes");
+    int64_t k = 0;
+    for (hipGraphNode_t node : nodes) {
+        hipGraphNodeType type;
+        check_hip(hipGraphNodeGetType(node, &type), "reading graph node type");
+        if (type == hipGraphNodeTypeKernel) ++k;
+    }
+    *kernels = k;
+    *total = static_cast<int64_t>(count);
+}
 
 [[noreturn]] void invalid(const std::string& message) { throw FluxError(FLUX_ERROR_INVALID_VALUE, message); }
 [[noreturn]] void bad_state(const std::string& message) { throw FluxError(FLUX_ERROR_STATE, message); }
@@ -62,6 +106,18 @@ int device_cu_count() {
     int cus = 0;
     check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device), "querying CU count");
     return cus;
+}
+
+void host_counters(int64_t* synchronizations, int64_t* allocations, int64_t* frees) {
+    *synchronizations = g_host_syncs.load(std::memory_order_relaxed);
+    *allocations = g_device_allocs.load(std::memory_order_relaxed);
+    *frees = g_device_frees.load(std::memory_order_relaxed);
+}
+
+void DecodeRuntime::graph_nodes(int64_t* kernels, int64_t* total) const { count_graph_nodes(graph_, kernels, total); }
+
+void LayerDecodeRuntime::graph_nodes(int64_t* kernels, int64_t* total) const {
+    count_graph_nodes(graph_, kernels, total);
 }
 
 int isolated_attention_chunks(int64_t capacity) {
@@ -125,11 +181,11 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
         check_hip(hipEventRecord(setup, stream), "recording setup event");
         check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
         check_hip(launch_fused_decode(args_, grid_, capture_stream_), "warming fused decode");
-        check_hip(hipStreamSynchronize(capture_stream_), "warming fused decode");
+        check_hip(counted_stream_sync(capture_stream_), "warming fused decode");
         check_hip(hipEventDestroy(setup), "destroying setup event");
         if (device_error() != 0) throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: warm-up step failed");
         initialize_state(initial_token, sources, position, capture_stream_, true);
-        check_hip(hipStreamSynchronize(capture_stream_), "initialising decode state");
+        check_hip(counted_stream_sync(capture_stream_), "initialising decode state");
 
         // Capture one token step (a single fused-kernel node) for replay().
         check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
@@ -140,7 +196,7 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
         check_hip(launch_status, "capturing fused decode step");
         check_hip(end_status, "ending graph capture");
         check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating decode graph");
-        check_hip(hipStreamSynchronize(capture_stream_), "finalising capture");
+        check_hip(counted_stream_sync(capture_stream_), "finalising capture");
     } catch (...) {
         release();
         throw;
@@ -153,16 +209,16 @@ void DecodeRuntime::release() noexcept {
     int previous = -1;
     (void)hipGetDevice(&previous);
     (void)hipSetDevice(device_);
-    if (pending_ && completion_ != nullptr) (void)hipEventSynchronize(completion_);
+    if (pending_ && completion_ != nullptr) (void)counted_event_sync(completion_);
     if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     if (graph_) (void)hipGraphDestroy(graph_);
     if (completion_) (void)hipEventDestroy(completion_);
     if (capture_stream_) {
-        (void)hipStreamSynchronize(capture_stream_);
+        (void)counted_stream_sync(capture_stream_);
         (void)hipStreamDestroy(capture_stream_);
     }
-    if (cache_block_) (void)hipFree(cache_block_);
-    if (state_block_) (void)hipFree(state_block_);
+    if (cache_block_) (void)counted_free(cache_block_);
+    if (state_block_) (void)counted_free(state_block_);
     graph_exec_ = nullptr;
     graph_ = nullptr;
     completion_ = nullptr;
@@ -173,7 +229,7 @@ void DecodeRuntime::release() noexcept {
 
 void DecodeRuntime::allocate() {
     const size_t cache_elems = static_cast<size_t>(kLayers) * kKVHeads * capacity_ * kHeadDim;
-    check_hip(hipMalloc(&cache_block_, 2 * cache_elems * sizeof(float)), "allocating K/V cache");
+    check_hip(counted_malloc(&cache_block_, 2 * cache_elems * sizeof(float)), "allocating K/V cache");
     key_cache_ = static_cast<float*>(cache_block_);
     value_cache_ = key_cache_ + cache_elems;
 
@@ -195,7 +251,7 @@ void DecodeRuntime::allocate() {
     const size_t o_layers = take(sizeof(LayerWeights) * kLayers);
     const size_t o_ll = take(ll_bytes_);
     state_bytes_ = offset;
-    check_hip(hipMalloc(&state_block_, state_bytes_), "allocating decode state");
+    check_hip(counted_malloc(&state_block_, state_bytes_), "allocating decode state");
     char* base = static_cast<char*>(state_block_);
     logits_ = reinterpret_cast<float*>(base + o_logits);
     input_token_ = reinterpret_cast<int64_t*>(base + o_token);
@@ -280,7 +336,7 @@ int64_t* DecodeRuntime::generate_greedy(int64_t decode_steps, hipStream_t stream
         launch_steps(decode_steps, stream, stream);
         if (elapsed_ms != nullptr) {
             check_hip(hipEventRecord(stop, stream), "recording timing event");
-            check_hip(hipEventSynchronize(stop), "waiting for timing event");
+            check_hip(counted_event_sync(stop), "waiting for timing event");
             check_hip(hipEventElapsedTime(elapsed_ms, start, stop), "reading timing events");
             (void)hipEventDestroy(start);
             (void)hipEventDestroy(stop);
@@ -308,11 +364,11 @@ void DecodeRuntime::reset(const int64_t* token, const CacheSources& sources, int
     }
     check_hip(hipSetDevice(device_), "hipSetDevice");
     if (pending_) {
-        check_hip(hipEventSynchronize(completion_), "waiting to reset full runtime");
+        check_hip(counted_event_sync(completion_), "waiting to reset full runtime");
         pending_ = false;
     }
     initialize_state(token, sources, position, stream, true);
-    check_hip(hipStreamSynchronize(stream), "resetting full runtime state");
+    check_hip(counted_stream_sync(stream), "resetting full runtime state");
     start_position_ = position;
     replay_count_ = 0;
     generation_started_ = false;
@@ -340,11 +396,11 @@ void DecodeRuntime::install_prefilled_state(const int64_t* token, int64_t positi
 
 int64_t DecodeRuntime::read_scalar(const int64_t* device_value) {
     check_hip(hipSetDevice(device_), "hipSetDevice");
-    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting to inspect runtime state");
+    if (pending_) check_hip(counted_event_sync(completion_), "waiting to inspect runtime state");
     int64_t result = -1;
-    check_hip(hipMemcpy(&result, device_value, sizeof(result), hipMemcpyDeviceToHost), "reading device state");
+    check_hip(counted_memcpy(&result, device_value, sizeof(result), hipMemcpyDeviceToHost), "reading device state");
     int32_t err = 0;
-    check_hip(hipMemcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
+    check_hip(counted_memcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
     if (err != 0)
         throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: device-side error " + std::to_string(err) +
                                                (err == 1 ? " (cross-workgroup wait timed out)"
@@ -354,9 +410,9 @@ int64_t DecodeRuntime::read_scalar(const int64_t* device_value) {
 
 int32_t DecodeRuntime::device_error() {
     check_hip(hipSetDevice(device_), "hipSetDevice");
-    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting for runtime");
+    if (pending_) check_hip(counted_event_sync(completion_), "waiting for runtime");
     int32_t err = 0;
-    check_hip(hipMemcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
+    check_hip(counted_memcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
     return err;
 }
 
@@ -429,7 +485,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
 
     // An empty-cache decode runtime at position 0 with a zero token.
     int64_t* zero_token = nullptr;
-    check_hip(hipMalloc(&block_, block_bytes_), "allocating prefill workspace");
+    check_hip(counted_malloc(&block_, block_bytes_), "allocating prefill workspace");
     char* base = static_cast<char*>(block_);
     hidden_a_ = reinterpret_cast<float*>(base + o_a);
     hidden_b_ = reinterpret_cast<float*>(base + o_b);
@@ -451,7 +507,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
         prefill(input_ids, stream);
     } catch (...) {
         decode_.reset();
-        (void)hipFree(block_);
+        (void)counted_free(block_);
         block_ = nullptr;
         throw;
     }
@@ -465,7 +521,7 @@ PrefillRuntime::~PrefillRuntime() {
         }
     }
     decode_.reset();
-    if (block_) (void)hipFree(block_);
+    if (block_) (void)counted_free(block_);
 }
 
 float* PrefillRuntime::prefill(const int64_t* input_ids, hipStream_t stream) {
@@ -604,7 +660,7 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
         const size_t o_partials = take(partial_floats * sizeof(float));
         block_bytes_ = offset;
         workspace_bytes_ = offset - o_query;
-        check_hip(hipMalloc(&block_, block_bytes_), "allocating layer decode buffers");
+        check_hip(counted_malloc(&block_, block_bytes_), "allocating layer decode buffers");
         char* base = static_cast<char*>(block_);
         input_hidden_ = reinterpret_cast<float*>(base + o_hidden);
         output_ = reinterpret_cast<float*>(base + o_output);
@@ -628,10 +684,10 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
         check_hip(hipEventRecord(setup, stream), "recording setup event");
         check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
         run_body(capture_stream_);
-        check_hip(hipStreamSynchronize(capture_stream_), "warming layer decode");
+        check_hip(counted_stream_sync(capture_stream_), "warming layer decode");
         check_hip(hipEventDestroy(setup), "destroying setup event");
         initialize_state(initial_hidden, key_source, value_source, source_length, position, capture_stream_, true);
-        check_hip(hipStreamSynchronize(capture_stream_), "initialising layer decode state");
+        check_hip(counted_stream_sync(capture_stream_), "initialising layer decode state");
 
         check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
         try {
@@ -644,7 +700,7 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
         }
         check_hip(hipStreamEndCapture(capture_stream_, &graph_), "ending graph capture");
         check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating layer graph");
-        check_hip(hipStreamSynchronize(capture_stream_), "finalising capture");
+        check_hip(counted_stream_sync(capture_stream_), "finalising capture");
     } catch (...) {
         release();
         throw;
@@ -657,15 +713,15 @@ void LayerDecodeRuntime::release() noexcept {
     int previous = -1;
     (void)hipGetDevice(&previous);
     (void)hipSetDevice(device_);
-    if (pending_ && completion_ != nullptr) (void)hipEventSynchronize(completion_);
+    if (pending_ && completion_ != nullptr) (void)counted_event_sync(completion_);
     if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     if (graph_) (void)hipGraphDestroy(graph_);
     if (completion_) (void)hipEventDestroy(completion_);
     if (capture_stream_) {
-        (void)hipStreamSynchronize(capture_stream_);
+        (void)counted_stream_sync(capture_stream_);
         (void)hipStreamDestroy(capture_stream_);
     }
-    if (block_) (void)hipFree(block_);
+    if (block_) (void)counted_free(block_);
     graph_exec_ = nullptr;
     graph_ = nullptr;
     completion_ = nullptr;
@@ -747,20 +803,20 @@ void LayerDecodeRuntime::reset(const float* hidden, const float* key_source, con
     validate_state(hidden, key_source, value_source, source_length, position);
     check_hip(hipSetDevice(device_), "hipSetDevice");
     if (pending_) {
-        check_hip(hipEventSynchronize(completion_), "waiting to reset runtime");
+        check_hip(counted_event_sync(completion_), "waiting to reset runtime");
         pending_ = false;
     }
     initialize_state(hidden, key_source, value_source, source_length, position, stream, true);
-    check_hip(hipStreamSynchronize(stream), "resetting runtime state");
+    check_hip(counted_stream_sync(stream), "resetting runtime state");
     start_position_ = position;
     replay_count_ = 0;
 }
 
 int64_t LayerDecodeRuntime::position() {
     check_hip(hipSetDevice(device_), "hipSetDevice");
-    if (pending_) check_hip(hipEventSynchronize(completion_), "waiting to inspect device position");
+    if (pending_) check_hip(counted_event_sync(completion_), "waiting to inspect device position");
     int64_t result = -1;
-    check_hip(hipMemcpy(&result, position_, sizeof(result), hipMemcpyDeviceToHost), "reading device position");
+    check_hip(counted_memcpy(&result, position_, sizeof(result), hipMemcpyDeviceToHost), "reading device position");
     return result;
 }
 

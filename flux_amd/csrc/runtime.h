@@ -56,6 +56,7 @@ public:
     int64_t replay_count() const { return replay_count_; }
     int64_t capacity() const { return capacity_; }
     void buffers(flux_decode_buffers* out) const;
+    void graph_nodes(int64_t* kernels, int64_t* total) const;
     int device() const { return device_; }
 
 private:
@@ -168,6 +169,7 @@ public:
     int64_t replay_count() const { return replay_count_; }
     int64_t capacity() const { return capacity_; }
     void buffers(flux_layer_decode_buffers* out) const;
+    void graph_nodes(int64_t* kernels, int64_t* total) const;
 
 private:
     void validate_state(const float* hidden, const float* key_source, const float* value_source,
@@ -211,6 +213,8 @@ private:
 };
 
 int device_cu_count();
+// Totals since load: host-blocking runtime calls, device allocations, device frees.
+void host_counters(int64_t* synchronizations, int64_t* allocations, int64_t* frees);
 // Key chunks of the isolated decode attention for `capacity` positions.
 int isolated_attention_chunks(int64_t capacity);
 

@@ -127,21 +127,44 @@ def _model_weights(model: nn.Module) -> tuple[_native.FluxWeights, list[float], 
     return weights, epsilons, scales
 
 
-class _DecodeHandle:
-    """Owns (or borrows) a ``flux_decode*`` and exposes its buffers as torch views."""
+class _NativeAllocation:
+    """Owns one native runtime object and destroys it when the last holder goes.
 
-    def __init__(self, raw: int, device: torch.device, owned: bool, keepalive: Any = None) -> None:
+    Zero-copy tensor views of runtime buffers hold this object (torch keeps the
+    view's ``__cuda_array_interface__`` owner alive from C++, which the garbage
+    collector cannot traverse), and this object holds nothing that holds the
+    views, so no reference cycle keeps device memory alive.  ``keepalive`` holds
+    what the native object borrows (model weights, RoPE tables).
+    """
+
+    def __init__(self, raw: int, destroy: str, keepalive: Any) -> None:
+        self.raw = ctypes.c_void_p(raw)
+        self._destroy = destroy
+        self.keepalive = keepalive
+
+    def __del__(self) -> None:
+        try:
+            if self.raw:
+                getattr(_native.load(), self._destroy)(self.raw)
+        except Exception:  # pragma: no cover - interpreter shutdown
+            pass
+        self.raw = ctypes.c_void_p(0)
+
+
+class _DecodeHandle:
+    """A ``flux_decode*`` (owned, or borrowed from a prefill runtime) and torch views of its buffers."""
+
+    def __init__(self, raw: int, device: torch.device, owner: _NativeAllocation) -> None:
         self.raw = ctypes.c_void_p(raw)
         self.device = device
-        self.owned = owned
-        self.keepalive = keepalive
+        self.owner = owner
         buffers = _native.DecodeBuffers()
         _native.check(_native.load().flux_decode_get_buffers(self.raw, ctypes.byref(buffers)))
         self.buffers = buffers
         cap, vocab = int(buffers.capacity), int(buffers.vocab_size)
         self.capacity = cap
         self.vocab_size = vocab
-        view = lambda address, shape, dtype: _native.device_tensor(address, shape, dtype, self, device)  # noqa: E731
+        view = lambda address, shape, dtype: _native.device_tensor(address, shape, dtype, owner, device)  # noqa: E731
         self.logits = view(buffers.logits, (1, 1, vocab), torch.float32)
         self.input_token = view(buffers.input_token, (1, 1), torch.int64)
         self.generated_tokens = view(buffers.generated_tokens, (cap,), torch.int64)
@@ -167,6 +190,12 @@ class _DecodeHandle:
         out = ctypes.c_int64()
         _native.check(_native.load().flux_decode_replay_count(self.raw, ctypes.byref(out)))
         return int(out.value)
+
+    def graph_nodes(self) -> tuple[int, int]:
+        """(kernel nodes, all nodes) of the captured one-step replay graph."""
+        kernels, total = ctypes.c_int64(), ctypes.c_int64()
+        _native.check(_native.load().flux_decode_graph_nodes(self.raw, ctypes.byref(kernels), ctypes.byref(total)))
+        return int(kernels.value), int(total.value)
 
     def replay(self, token: torch.Tensor | None) -> torch.Tensor:
         if token is not None:
@@ -198,42 +227,21 @@ class _DecodeHandle:
             _native.check(_native.load().flux_decode_device_error(self.raw, ctypes.byref(out)))
         return int(out.value)
 
-    def close(self) -> None:
-        if self.owned and self.raw:
-            _native.load().flux_decode_destroy(self.raw)
-        self.raw = ctypes.c_void_p(0)
-
-    def __del__(self) -> None:
-        try:
-            self.close()
-        except Exception:  # pragma: no cover - interpreter shutdown
-            pass
-
 
 class _PrefillHandle:
     def __init__(self, raw: int, device: torch.device, keepalive: Any) -> None:
-        self.raw = ctypes.c_void_p(raw)
+        self.owner = _NativeAllocation(raw, "flux_prefill_destroy", keepalive)
+        self.raw = self.owner.raw
         self.device = device
-        self.keepalive = keepalive
         buffers = _native.PrefillBuffers()
         _native.check(_native.load().flux_prefill_get_buffers(self.raw, ctypes.byref(buffers)))
         self.buffers = buffers
         decode_raw = _native.load().flux_prefill_decode(self.raw)
-        self.decode = _DecodeHandle(decode_raw, device, owned=False, keepalive=self)
+        self.decode = _DecodeHandle(decode_raw, device, self.owner)
         vocab = self.decode.vocab_size
-        self.logits = _native.device_tensor(buffers.prefill_logits, (1, 1, vocab), torch.float32, self, device)
-        self.final_hidden = _native.device_tensor(buffers.final_hidden, (1, 1, 576), torch.float32, self, device)
-
-    def close(self) -> None:
-        if self.raw:
-            _native.load().flux_prefill_destroy(self.raw)
-        self.raw = ctypes.c_void_p(0)
-
-    def __del__(self) -> None:
-        try:
-            self.close()
-        except Exception:  # pragma: no cover
-            pass
+        self.logits = _native.device_tensor(buffers.prefill_logits, (1, 1, vocab), torch.float32, self.owner, device)
+        self.final_hidden = _native.device_tensor(buffers.final_hidden, (1, 1, 576), torch.float32, self.owner,
+                                                  device)
 
 
 class NativeSmolLM2Prefill:
@@ -450,8 +458,8 @@ class NativeSmolLM2Decode:
                 _native.pointer_array(value_caches), _native.length_array([k.shape[2] for k in key_caches]),
                 _native.double_array(epsilons), _native.double_array(scales), _native.current_stream(device),
                 ctypes.byref(raw)))
-        self._handle = _DecodeHandle(raw.value, device, owned=True,
-                                     keepalive=(model, self._rope_cos, self._rope_sin))
+        owner = _NativeAllocation(raw.value, "flux_decode_destroy", (model, self._rope_cos, self._rope_sin))
+        self._handle = _DecodeHandle(raw.value, device, owner)
         self.prefill_logits = None
         self.prefill_input_ids = None
         self._prefill_cache = None
@@ -699,13 +707,14 @@ class NativeSmolLM2LayerDecode:
                 _native.ptr(initial_hidden), _native.ptr(initial_key_cache), _native.ptr(initial_value_cache),
                 int(initial_key_cache.shape[2]), float(epsilon), float(attention_scale),
                 _native.current_stream(device), ctypes.byref(raw)))
-        self._raw = raw
-        # The runtime borrows the weights and tables: keep them alive with it.
-        self._keepalive = tuple(t for t, _, _ in weights)
+        # The runtime borrows the weights and tables: its allocation keeps them alive.
+        self._owner = _NativeAllocation(raw.value, "flux_layer_decode_destroy", tuple(t for t, _, _ in weights))
+        self._raw = self._owner.raw
         buffers = _native.LayerDecodeBuffers()
         _native.check(_native.load().flux_layer_decode_get_buffers(self._raw, ctypes.byref(buffers)))
         self._buffers = buffers
-        view = lambda address, shape, dtype: _native.device_tensor(address, shape, dtype, self, device)  # noqa: E731
+        owner = self._owner
+        view = lambda address, shape, dtype: _native.device_tensor(address, shape, dtype, owner, device)  # noqa: E731
         self._output = view(buffers.output, (1, 1, 576), torch.float32)
         self._input_hidden = view(buffers.input_hidden, (1, 1, 576), torch.float32)
         self._key_cache = view(buffers.key_cache, (1, 3, capacity, 64), torch.float32)
@@ -787,17 +796,13 @@ class NativeSmolLM2LayerDecode:
     def workspace_bytes(self) -> int:
         return int(self._buffers.workspace_bytes)
 
-    def close(self) -> None:
-        raw = getattr(self, "_raw", None)
-        if raw:
-            _native.load().flux_layer_decode_destroy(raw)
-        self._raw = ctypes.c_void_p(0)
+    def graph_nodes(self) -> tuple[int, int]:
+        """(kernel nodes, all nodes) of the captured layer-step graph."""
+        kernels, total = ctypes.c_int64(), ctypes.c_int64()
+        _native.check(_native.load().flux_layer_decode_graph_nodes(self._raw, ctypes.byref(kernels),
+                                                                   ctypes.byref(total)))
+        return int(kernels.value), int(total.value)
 
-    def __del__(self) -> None:
-        try:
-            self.close()
-        except Exception:  # interpreter shutdown
-            pass
 
 
 def native_smollm2_greedy_generate(model: nn.Module, input_ids: torch.Tensor, *, max_new_tokens: int) -> torch.Tensor:

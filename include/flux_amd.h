@@ -150,6 +150,14 @@ int flux_decode_get_buffers(const flux_decode* runtime, flux_decode_buffers* out
 /* Wait for outstanding work and return the device error word (0 = none). */
 int flux_decode_device_error(flux_decode* runtime, int32_t* out);
 /* Time the next `decode_steps` steps with events on `stream` (benchmark aid). */
+/* Nodes of the captured replay graph: kernel nodes (the launches per replay) and all
+ * nodes.  Counterpart of the launch count the reference's runtime audit takes with
+ * torch.profiler (benchmarks/benchmark_flux.py:818-859). */
+int flux_decode_graph_nodes(const flux_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes);
+/* Process-wide totals since load of the runtimes' host-blocking calls (stream/event
+ * synchronisation, synchronous copies), device allocations and frees; the audit
+ * compares them around replays (benchmarks/benchmark_flux.py:838-858). */
+int flux_host_counters(int64_t* synchronizations, int64_t* allocations, int64_t* frees);
 int flux_decode_generate_greedy_timed(flux_decode* runtime, int64_t decode_steps, hipStream_t stream,
                                       float* milliseconds);
 void flux_decode_destroy(flux_decode* runtime);
@@ -231,6 +239,7 @@ int flux_layer_decode_position(flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_replay_count(const flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_capacity(const flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_decode_buffers* out);
+int flux_layer_decode_graph_nodes(const flux_layer_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes);
 void flux_layer_decode_destroy(flux_layer_decode* runtime);
 
 /* ------------------------------------------------------------------------ */

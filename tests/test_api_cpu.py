@@ -157,3 +157,10 @@ def test_layer_decode_requires_gpu_tensors():
                                  torch.ones(576), torch.zeros(3072, 576), torch.zeros(576, 1536), torch.zeros(8, 64),
                                  torch.zeros(8, 64), torch.zeros(1, 3, 0, 64), torch.zeros(1, 3, 0, 64), 8, 0, 1e-5,
                                  0.125)
+
+
+def test_audit_argument_validation():
+    from flux_amd.runtime.audit import runtime_audit
+
+    with pytest.raises(ValueError, match="audit capacity must exceed audit replays plus three warmups"):
+        runtime_audit(_model(), capacity=10, replays=7)
