@@ -48,7 +48,7 @@ __device__ __forceinline__ unsigned tid_opaque() {
 constexpr int kThreads = 512;
 constexpr int kWavesPerWG = kThreads / kWave;
 constexpr int kAttnRows = 224;            // attention rows per workgroup (LDS-resident K/V)
-constexpr int kLmBatch = 8;
+constexpr int kLmBatch = 4;
 constexpr uint64_t kTimeoutTicks = 20ull * 1000 * 1000;  // 200 ms of the 100 MHz wall clock
 
 // ---------------------------------------------------------------------------
@@ -570,28 +570,60 @@ __device__ __forceinline__ void chunk_range(int64_t attended, int chunks, int c,
 
 // ---------------------------------------------------------------------------
 // LM head + argmax: rows [row0, row1) for one wave, batches of kLmBatch rows.
+// Rows [row0, row1) of the LM head, kLmBatch rows per stage, two stages in
+// flight: the next stage's rows are requested before the current stage's dot
+// products, so HBM keeps streaming while a wave computes.  `w` holds the first
+// stage on entry (rows row0..row0+kLmBatch-1, clamped like below).
+template <class LogitsOut>
+__device__ __forceinline__ void lm_stage(const float (&x)[9], const float (&w)[kLmBatch][9], int64_t base, int64_t row1,
+                                         const LogitsOut& logits, float& best_v, int64_t& best_i) {
+    const int lane = tid_opaque() & 63;
+#pragma unroll
+    for (int r = 0; r < kLmBatch; ++r) {
+        const float v = wave_sum(dot_lane<9>(x, w[r]));
+        const int64_t row = base + r;
+        if (row < row1) {
+            if (lane == 0) logits.put(row, v);
+            if (argmax_precedes(v, row, best_v, best_i)) {
+                best_v = v;
+                best_i = row;
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void lm_load(const float* __restrict__ lm_head, int64_t base, int64_t row1, int lane,
+                                        float (&w)[kLmBatch][9]) {
+#pragma unroll
+    for (int r = 0; r < kLmBatch; ++r) {
+        const int64_t row = base + r < row1 ? base + r : (row1 > 0 ? row1 - 1 : 0);
+        load_row576(lm_head + row * kHidden, lane, w[r]);
+    }
+}
+
+template <class LogitsOut>
+__device__ __forceinline__ void lm_rows_pipelined(const float* __restrict__ lm_head, const float (&x)[9],
+                                                  float (&wa)[kLmBatch][9], int64_t row0, int64_t row1, int lane,
+                                                  const LogitsOut& logits, float& best_v, int64_t& best_i) {
+    float wb[kLmBatch][9];
+    for (int64_t base = row0; base < row1; base += 2 * kLmBatch) {
+        const bool next_b = base + kLmBatch < row1;
+        if (next_b) lm_load(lm_head, base + kLmBatch, row1, lane, wb);
+        lm_stage(x, wa, base, row1, logits, best_v, best_i);
+        if (!next_b) break;
+        const bool next_a = base + 2 * kLmBatch < row1;
+        if (next_a) lm_load(lm_head, base + 2 * kLmBatch, row1, lane, wa);
+        lm_stage(x, wb, base + kLmBatch, row1, logits, best_v, best_i);
+    }
+}
+
 template <class LogitsOut>
 __device__ __forceinline__ void lm_rows(const float* __restrict__ lm_head, const float (&x)[9], int64_t row0, int64_t row1,
                                         int lane, const LogitsOut& logits, float& best_v, int64_t& best_i) {
     for (int64_t base = row0; base < row1; base += kLmBatch) {
         float w[kLmBatch][9];
-#pragma unroll
-        for (int r = 0; r < kLmBatch; ++r) {
-            const int64_t row = base + r < row1 ? base + r : row1 - 1;
-            load_row576(lm_head + row * kHidden, lane, w[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < kLmBatch; ++r) {
-            const float v = wave_sum(dot_lane<9>(x, w[r]));
-            const int64_t row = base + r;
-            if (row < row1) {
-                if (lane == 0) logits.put(row, v);
-                if (argmax_precedes(v, row, best_v, best_i)) {
-                    best_v = v;
-                    best_i = row;
-                }
-            }
-        }
+        lm_load(lm_head, base, row1, lane, w);
+        lm_stage(x, w, base, row1, logits, best_v, best_i);
     }
 }
 
@@ -998,16 +1030,11 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             const int64_t row1 = row0 + per < args.vocab ? row0 + per : args.vocab;
             const int layer = kLayers;
             FLUX_TRACE_POINT(0);
-            // The first kLmPrefetch rows of this wave are loaded before waiting for h.
-            constexpr int kLmPrefetch = 8;
-            float wl[kLmPrefetch][9];
+            // The first kLmBatch rows of this wave are loaded before waiting for h.
+            float wl[kLmBatch][9];
             float wn[9];
             load_slice576(args.final_norm, lane, wn);
-#pragma unroll
-            for (int r = 0; r < kLmPrefetch; ++r) {
-                const int64_t row = row0 + r < row1 ? row0 + r : (row1 > row0 ? row1 - 1 : 0);
-                load_row576(args.lm_head + row * kHidden, lane, wl[r]);
-            }
+            lm_load(args.lm_head, row0, row1, lane, wl);
             wg_ll_fetch<2>(ll_last + LLLayout::kHidden, kHidden, Contiguous{}, ep_last, wctx, hvec);
             __syncthreads();
             FLUX_TRACE_POINT(1);
@@ -1016,21 +1043,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             norm_slice_w(h, wn, args.final_eps, x);
             float best_v = -INFINITY;
             int64_t best_i = INT64_MAX;
-#pragma unroll
-            for (int r = 0; r < kLmPrefetch; ++r) {
-                const float v = wave_sum(dot_lane<9>(x, wl[r]));
-                const int64_t row = row0 + r;
-                if (row < row1) {
-                    if (lane == 0) args.logits[row] = v;
-                    if (argmax_precedes(v, row, best_v, best_i)) {
-                        best_v = v;
-                        best_i = row;
-                    }
-                }
-            }
-            if (row0 + kLmPrefetch < row1)
-                lm_rows(args.lm_head, x, row0 + kLmPrefetch, row1, lane, LogitsPlainOut{args.logits}, best_v,
-                        best_i);
+            lm_rows_pipelined(args.lm_head, x, wl, row0, row1, lane, LogitsPlainOut{args.logits}, best_v, best_i);
             wg_argmax(best_v, best_i, red_v, red_i);
             FLUX_TRACE_POINT(2);
             // This token's K/V cache rows were written through (agent-scope stores); wait
