@@ -14,8 +14,8 @@
 //    wave hold columns j and j+32 of the same rows, which is exactly the RoPE pair
 //    (a 64-column group = one head) and the gate/up pair (gate/up rows are
 //    interleaved 32+32 per group).
-//  * Attention: one block per (64-query tile, query head); 4 waves x 16 queries.
-//    S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x4f32, so the S^T
+//  * Attention: one block per (128-query tile, query head, key chunk); 4 waves x 32
+//    queries.  S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x2f32, so the S^T
 //    accumulators are already the B operand of the PV product (no transpose).
 
 #include "flux_common.h"
@@ -23,6 +23,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <type_traits>
 
 namespace flux {
 namespace {
@@ -221,221 +222,363 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA prefill attention.  The keys of a query tile are split into chunks of
-// at most kChunkTiles key tiles; every (query tile, head, chunk) is one block, so
-// no block streams more than 2048 keys (the causal tail would otherwise be one
-// block per head walking all S keys).  A query tile with one chunk writes its rows
-// directly; longer ones write (o, m, l) partials that prefill_attention_merge_kernel
-// combines (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu splits the keys
-// into partitions and merges them the same way).
-constexpr int kQTile = 64;
+// Causal GQA prefill attention on v_mfma_f32_32x32x2f32.
+//
+// Block = (128-query tile, query head, chunk of at most kChunkTiles 64-key tiles);
+// 4 waves x 32 queries.  Per 64-key tile a wave computes S^T = K Q^T as two 32x32
+// tiles (32 MFMAs each: instruction s pairs dims s and s + 32), then
+// O^T += V^T P^T (16 MFMAs per 32 keys and 32-dim half): the S^T accumulator of a
+// lane is exactly the B operand of the PV product, so P never leaves registers.
+// O^T rows are dims 2i + db (db = 0, 1), so a lane's two V operands of one key are
+// adjacent floats.  Q is pre-scaled by scale * log2(e) so scores are already in
+// exp2 units.
+//
+// K/V tiles stream HBM -> LDS with global_load_lds: one K buffer, refilled with the
+// next tile as soon as every wave has finished its S^T, and two V buffers, the
+// next tile's copied while this tile's is read.  Each buffer is its own LDS
+// variable, so reads of one never wait on copies into another.  Three blocks fit a
+// CU (49 KB of LDS, at most 168 VGPRs), i.e. three waves per SIMD.
+//
+// A query tile's keys are split into chunks of kChunkTiles tiles; a tile with one
+// chunk writes its rows directly, longer ones write (o, m, l) partials that
+// prefill_attention_merge_kernel combines
+// (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu splits the keys into
+// partitions and merges them the same way).  Items (query tile, chunk) are
+// launched longest first so the tail of the grid is short chunks.
+constexpr int kQTile = 128;
 constexpr int kKTile = 64;
 constexpr int kAttnThreads = 256;
-constexpr int kKVPad = 4;
-constexpr int kChunkTiles = 32;
+constexpr int kChunkTiles = 24;
 constexpr int kPartialRow = kHeadDim + 2;  // o[64], m, l
+constexpr int kMergeMaxChunks = 16;        // kMaxCapacity / (kChunkTiles * kKTile)
+constexpr int kKVTileFloats = kKTile * kHeadDim;
 
 __host__ __device__ __forceinline__ int64_t attn_q_tiles(int64_t seq) { return (seq + kQTile - 1) / kQTile; }
-__host__ __device__ __forceinline__ int64_t attn_max_chunks(int64_t seq) {
-    return (attn_q_tiles(seq) + kChunkTiles - 1) / kChunkTiles;
+__host__ __device__ __forceinline__ int64_t attn_key_tiles(int64_t seq, int64_t qt) {
+    const int64_t last = (qt + 1) * kQTile - 1 < seq - 1 ? (qt + 1) * kQTile - 1 : seq - 1;
+    return last / kKTile + 1;
 }
-// Blocks of chunk c: query tiles qt >= c * kChunkTiles, times the query heads.
-__host__ __device__ __forceinline__ int64_t attn_chunk_blocks(int64_t seq, int64_t c) {
-    return (attn_q_tiles(seq) - c * kChunkTiles) * kQHeads;
+__host__ __device__ __forceinline__ int64_t attn_chunks(int64_t seq, int64_t qt) {
+    return (attn_key_tiles(seq, qt) + kChunkTiles - 1) / kChunkTiles;
 }
-// Partial slot of (qt, h, c) for query tiles with more than one chunk.
+// Query tiles below kLongTile have a single chunk.
+constexpr int64_t kLongTile = kChunkTiles * kKTile / kQTile;  // 12
+__host__ __device__ __forceinline__ int64_t attn_max_chunks(int64_t seq) { return attn_chunks(seq, attn_q_tiles(seq) - 1); }
 __host__ __device__ __forceinline__ int64_t attn_partial_slot(int64_t seq, int64_t qt, int h, int64_t c) {
-    return ((qt - kChunkTiles) * kQHeads + h) * attn_max_chunks(seq) + c;
+    return ((qt - kLongTile) * kQHeads + h) * attn_max_chunks(seq) + c;
+}
+// Items of one head, longest first: every chunk of the last query tile, then the
+// full chunks of the others (chunk-major), then their partial last chunks by
+// decreasing length.  Inner query tiles have 2 (qt + 1) key tiles.
+__host__ __device__ __forceinline__ int64_t attn_items(int64_t seq) {
+    const int64_t q_tiles = attn_q_tiles(seq);
+    int64_t n = attn_chunks(seq, q_tiles - 1);
+    for (int64_t qt = 0; qt + 1 < q_tiles; ++qt) n += attn_chunks(seq, qt);
+    return n;
+}
+__device__ __forceinline__ void attn_item(int64_t seq, int64_t i, int64_t& qt, int64_t& chunk) {
+    const int64_t q_tiles = attn_q_tiles(seq);
+    const int64_t last_chunks = attn_chunks(seq, q_tiles - 1);
+    if (i < last_chunks) {
+        qt = q_tiles - 1;
+        chunk = i;
+        return;
+    }
+    i -= last_chunks;
+    // Full chunk c of inner tile qt needs 2 (qt + 1) >= kChunkTiles (c + 1).
+    for (int64_t c = 0;; ++c) {
+        const int64_t first = kChunkTiles / 2 * (c + 1) - 1;
+        const int64_t count = q_tiles - 1 - first > 0 ? q_tiles - 1 - first : 0;
+        if (count == 0) break;
+        if (i < count) {
+            qt = first + i;
+            chunk = c;
+            return;
+        }
+        i -= count;
+    }
+    // Partial chunks: length 2 (qt + 1) mod kChunkTiles = len, longest first.
+    for (int64_t len = kChunkTiles - 2; len >= 2; len -= 2) {
+        const int64_t r0 = len / 2 - 1;
+        const int64_t count = q_tiles - 2 - r0 >= 0 ? (q_tiles - 2 - r0) / (kChunkTiles / 2) + 1 : 0;
+        if (i < count) {
+            qt = r0 + (kChunkTiles / 2) * i;
+            chunk = 2 * (qt + 1) / kChunkTiles;
+            return;
+        }
+        i -= count;
+    }
+    qt = 0;  // not reached for i < attn_items(seq)
+    chunk = 0;
 }
 
-__global__ void __launch_bounds__(kAttnThreads) prefill_attention_kernel(const float* __restrict__ q,
-                                                                         const float* __restrict__ key_cache,
-                                                                         const float* __restrict__ value_cache,
-                                                                         int64_t seq, int64_t capacity, float scale,
-                                                                         float* __restrict__ workspace,
-                                                                         float* __restrict__ out_rows) {
-    __shared__ __align__(16) float k_s[kKTile][kHeadDim + kKVPad];
-    __shared__ __align__(16) float v_s[kKTile][kHeadDim + kKVPad];
+// LDS tiles: K rows are padded to 17 16-byte pieces (68 words), so the 32 lanes that
+// read one piece of 32 consecutive rows hit distinct banks; V rows are plain (the 32
+// lanes of a V read cover one whole row).  Every read is a per-lane base plus an
+// immediate offset.
+constexpr int kKRow = kHeadDim + 4;                    // words per padded K row
+constexpr int kKTileWords = kKTile * kKRow;           // 4352
+constexpr int kKCopies = kKTileWords / 256;           // 17 global_load_lds of 1 KB
+constexpr int kVCopies = kKVTileFloats / 256;         // 16
+
+// max / sum of the values of lanes l and l ^ 32 (v_permlane32_swap: r[0] holds the
+// low half's values in both halves, r[1] the high half's).
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup barrier for LDS hand-offs: this wave's LDS reads are complete and no
+// memory access moves across it; global-memory copies still in flight are not
+// waited for (each wave waits for its own with vmcnt where needed).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)))
+prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ key_cache,
+                         const float* __restrict__ value_cache, int64_t seq, int64_t capacity, float scale,
+                         float* __restrict__ workspace, float* __restrict__ out_rows) {
+    __shared__ __align__(16) float ks[kKTileWords];
+    __shared__ __align__(16) float v0s[kKVTileFloats];
+    __shared__ __align__(16) float v1s[kKVTileFloats];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t q_tiles = attn_q_tiles(seq);
-    // Block b -> chunk c (chunk-major), then q tile (longest first) and head.
-    int64_t idx = blockIdx.x;
-    int64_t chunk = 0;
-    while (idx >= attn_chunk_blocks(seq, chunk)) {
-        idx -= attn_chunk_blocks(seq, chunk);
-        ++chunk;
-    }
-    const int64_t qt = q_tiles - 1 - idx / kQHeads;
-    const int h = static_cast<int>(idx % kQHeads);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = static_cast<int>(blockIdx.x % kQHeads);
+    int64_t qt, chunk;
+    attn_item(seq, blockIdx.x / kQHeads, qt, chunk);
     const int g = h / kGroup;
-    const int64_t q0 = qt * kQTile;
-    const int64_t row_base = q0 + wave * 16;
-    const int64_t my_row = row_base + (lane & 15);  // query row of this lane in S^T / O^T layouts
+    const int64_t qw0 = qt * kQTile + 32 * wave;  // first query of this wave
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int64_t my_q = qw0 + col;
 
-    // B operand of S^T = K Q^T.  MFMA instruction s pairs k-slot jg = lane/16 with
-    // dim 16 jg + s, so qreg[s] = Q[row = lane%16][16 jg + s] and a lane reads its 16
-    // K values of a key row with four ds_read_b128.
-    const int jg = lane >> 4;
-    float qreg[16];
+    // B operand of S^T = K Q^T: qreg[s] = Q[my_q][s + 32 half] * scale * log2(e).
+    float qreg[32];
     {
-        const int64_t r = my_row < seq ? my_row : seq - 1;
-        const float* qp = q + (static_cast<int64_t>(h) * seq + r) * kHeadDim + 16 * jg;
+        const int64_t r = my_q < seq ? my_q : seq - 1;
+        const float* qp = q + (static_cast<int64_t>(h) * seq + r) * kHeadDim + 32 * half;
+        const float s2 = scale * kLog2e;
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            const float4 v = *reinterpret_cast<const float4*>(qp + 4 * s4);
-            qreg[4 * s4] = v.x;
-            qreg[4 * s4 + 1] = v.y;
-            qreg[4 * s4 + 2] = v.z;
-            qreg[4 * s4 + 3] = v.w;
+        for (int t = 0; t < 8; ++t) {
+            const float4 v = *reinterpret_cast<const float4*>(qp + 4 * t);
+            qreg[4 * t] = v.x * s2;
+            qreg[4 * t + 1] = v.y * s2;
+            qreg[4 * t + 2] = v.z * s2;
+            qreg[4 * t + 3] = v.w * s2;
         }
     }
 
     const float* kg = key_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
     const float* vg = value_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
+    const int64_t k_tiles = attn_key_tiles(seq, qt);
+    const int64_t kt_begin = chunk * kChunkTiles;
+    const int64_t kt_end = kt_begin + kChunkTiles < k_tiles ? kt_begin + kChunkTiles : k_tiles;
 
-    f32x4 o_acc[4];
+    // Copies of key tile kt: K slot s (16 bytes) of the padded tile holds piece s % 17
+    // of row s / 17 (piece 16 is padding and repeats piece 0); V slot s holds piece
+    // s % 16 of row s / 16.  Copy i covers slots 64 i .. 64 i + 63; wave w issues
+    // copies w, w + 4, ...  Rows past the prompt repeat its last row (they are masked).
+    auto issue_k = [&](int64_t kt) {
+        const int k0 = static_cast<int>(kt) * kKTile;
+        const int last = static_cast<int>(seq) - 1 - k0;  // last valid row of the tile
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o_acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < (kKCopies + 3) / 4; ++j) {
+            const int i = wave + 4 * j;
+            if (i < kKCopies) {
+                const int slot = 64 * i + lane;
+                int row = slot / 17;
+                int piece = slot - 17 * row;
+                piece = piece == 16 ? 0 : piece;
+                row = row < last ? row : last;
+                __builtin_amdgcn_global_load_lds(kg + static_cast<int64_t>(k0 + row) * kHeadDim + 4 * piece,
+                                                 ks + 256 * i, 16, 0, 0);
+            }
+        }
+    };
+    auto issue_v = [&](float* vbuf, int64_t kt) {
+        const int k0 = static_cast<int>(kt) * kKTile;
+        const int last = static_cast<int>(seq) - 1 - k0;
+#pragma unroll
+        for (int j = 0; j < kVCopies / 4; ++j) {
+            const int i = wave + 4 * j;
+            int row = 4 * i + (lane >> 4);
+            row = row < last ? row : last;
+            __builtin_amdgcn_global_load_lds(vg + static_cast<int64_t>(k0 + row) * kHeadDim + 4 * (lane & 15),
+                                             vbuf + 256 * i, 16, 0, 0);
+        }
+    };
+
+    f32x16 o_acc[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[db][r] = 0.0f;
     float m_run = -INFINITY;
     float l_run = 0.0f;
 
-    const float scale2 = scale * kLog2e;  // scores in log2 units
-    const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
-    const int64_t k_tiles = last_key / kKTile + 1;
-    const int64_t kt_begin = chunk * kChunkTiles;
-    const int64_t kt_end = kt_begin + kChunkTiles < k_tiles ? kt_begin + kChunkTiles : k_tiles;
-    for (int64_t kt = kt_begin; kt < kt_end; ++kt) {
-        const int64_t k0 = kt * kKTile;
-        __syncthreads();
-        // Stage K and V tiles (64 x 64 each): 1024 float4 per tile, 4 per thread.
+    const int seq32 = static_cast<int>(seq);
+    const int qw = static_cast<int>(qw0);
+    const int q_me = static_cast<int>(my_q);
+    // QK of one tile: both 32-key halves when the second is visible to the wave (the
+    // two accumulator chains alternate), the K operands of step t + 1 read from LDS
+    // before the MFMAs of step t.
+    auto qk = [&](const float* ks, f32x16* s_acc, auto both_c) {
+        constexpr bool both = decltype(both_c)::value;
+        const float* k0p = ks + col * kKRow + 32 * half;  // row col, dims 32 half ..
+        const float* k1p = k0p + 32 * kKRow;                // row 32 + col
+        f32x4 ka = *reinterpret_cast<const f32x4*>(k0p);
+        f32x4 kb;
+        if constexpr (both) kb = *reinterpret_cast<const f32x4*>(k1p);
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int idx = threadIdx.x + it * kAttnThreads;
-            const int row = idx >> 4;
-            const int col = (idx & 15) * 4;
-            const int64_t key = k0 + row;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (key < seq) {
-                kv = *reinterpret_cast<const float4*>(kg + key * kHeadDim + col);
-                vv = *reinterpret_cast<const float4*>(vg + key * kHeadDim + col);
+        for (int t = 0; t < 8; ++t) {
+            f32x4 na, nb;
+            if (t < 7) {
+                na = *reinterpret_cast<const f32x4*>(k0p + 4 * (t + 1));
+                if constexpr (both) nb = *reinterpret_cast<const f32x4*>(k1p + 4 * (t + 1));
             }
-            *reinterpret_cast<float4*>(&k_s[row][col]) = kv;
-            *reinterpret_cast<float4*>(&v_s[row][col]) = vv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[e], qreg[4 * t + e], s_acc[0], 0, 0, 0);
+                if constexpr (both)
+                    s_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[e], qreg[4 * t + e], s_acc[1], 0, 0, 0);
+            }
+            if (t < 7) {
+                ka = na;
+                if constexpr (both) kb = nb;
+            }
         }
-        __syncthreads();
-
-        // S^T tile: 4 key blocks of 16 x (16 rows), K-dim 64 = 16 MFMA steps.
-        f32x4 s_acc[4];
+    };
+    // One key tile: S^T from the K tile, an LDS barrier after which the K buffer is
+    // refilled with the next tile, then softmax and O^T += V^T P^T from this tile's
+    // V buffer.  Waves whose queries all precede the tile skip the math but not the
+    // barriers.
+    auto tile = [&](const float* vs, int64_t kt, int64_t kt_next) {
+        const int k0 = static_cast<int>(kt) * kKTile;
+        const bool active = k0 <= qw + 31;
+        const bool need_mask = k0 + kKTile - 1 > qw || k0 + kKTile > seq32;
+        const bool live1 = k0 + 32 <= qw + 31;  // second 32-key half visible to some query
+        f32x16 s_acc[2];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const float* krow = &k_s[kb * 16 + (lane & 15)][16 * jg];
-            f32x4 kr[4];
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) kr[t] = *reinterpret_cast<const f32x4*>(krow + 4 * t);
-            s_acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < 16; ++r) s_acc[kb][r] = 0.0f;
+        if (live1)
+            qk(ks, s_acc, std::true_type{});
+        else if (active)
+            qk(ks, s_acc, std::false_type{});
+        lds_barrier();  // every wave is done with the K tile
+        issue_k(kt_next);
+        if (!active) return;
+        // Lane holds keys k0 + 32 kb + 8 (r / 4) + 4 half + r % 4 of query my_q.
+        if (!live1) {
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
-                s_acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s >> 2][s & 3], qreg[s], s_acc[kb], 0, 0, 0);
+            for (int r = 0; r < 16; ++r) s_acc[1][r] = -INFINITY;
         }
-        // Scale + causal mask; lane holds keys k0 + 16kb + 4(lane/16) + r for row my_row.
+        if (need_mask) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 32 * kb + 8 * (r >> 2) + 4 * half + (r & 3);
+                    s_acc[kb][r] = (key <= q_me && key < seq32) ? s_acc[kb][r] : -INFINITY;
+                }
+            }
+        }
         float tile_max = -INFINITY;
-        if (k0 + kKTile - 1 <= row_base) {  // every key of the tile precedes every query of the wave
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    s_acc[kb][r] *= scale2;
-                    tile_max = fmaxf(tile_max, s_acc[kb][r]);
-                }
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t key = k0 + 16 * kb + 4 * (lane >> 4) + r;
-                    const float v = (key <= my_row && key < seq) ? s_acc[kb][r] * scale2 : -INFINITY;
-                    s_acc[kb][r] = v;
-                    tile_max = fmaxf(tile_max, v);
-                }
-            }
-        }
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, kWave));
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, kWave));
-        const float m_new = fmaxf(m_run, tile_max);
-        const float alpha = m_new == -INFINITY ? 1.0f : (m_run == -INFINITY ? 0.0f : fast_exp2(m_run - m_new));
+            for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s_acc[kb][r]);
+        tile_max = halves_max(tile_max);
+        const float m_new = fmaxf(m_run, tile_max);  // finite: the first key of a chunk precedes every query
+        const float alpha = fast_exp2(m_run - m_new);
         float psum = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = s_acc[kb][r] == -INFINITY ? 0.0f : fast_exp2(s_acc[kb][r] - m_new);
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(s_acc[kb][r] - m_new);
                 s_acc[kb][r] = p;
                 psum += p;
             }
         }
-        psum += __shfl_xor(psum, 16, kWave);
-        psum += __shfl_xor(psum, 32, kWave);
+        psum = halves_sum(psum);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        // alpha is exactly 1 where the running max did not move: skip the rescale
+        // when that holds for every lane (multiplying by 1 would not change a bit).
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o_acc[db] *= alpha;
-        // O^T += V^T P^T: k-step (kb, r) uses keys 16kb + 4(lane/16) + r.
+            for (int db = 0; db < 2; ++db) o_acc[db] *= alpha;
+        }
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
+            if (kb == 1 && !live1) continue;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int krow = 16 * kb + 4 * (lane >> 4) + r;
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const float a = v_s[krow][16 * db + (lane & 15)];
-                    o_acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s_acc[kb][r], o_acc[db], 0, 0, 0);
-                }
+            for (int r = 0; r < 16; ++r) {
+                const float2 v = *reinterpret_cast<const float2*>(vs + (4 * half) * kHeadDim + 2 * col +
+                                                                  (32 * kb + 8 * (r >> 2) + (r & 3)) * kHeadDim);
+                o_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.x, s_acc[kb][r], o_acc[0], 0, 0, 0);
+                o_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v.y, s_acc[kb][r], o_acc[1], 0, 0, 0);
             }
         }
+    };
+
+    issue_k(kt_begin);
+    issue_v(v0s, kt_begin);
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    for (int64_t kt = kt_begin; kt < kt_end; kt += 2) {
+        const int64_t n1 = kt + 1 < kt_end ? kt + 1 : kt_end - 1;
+        issue_v(v1s, n1);
+        tile(v0s, kt, n1);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile kt + 1 have landed
+        lds_barrier();
+        if (kt + 1 < kt_end) {
+            const int64_t n2 = kt + 2 < kt_end ? kt + 2 : kt_end - 1;
+            issue_v(v0s, n2);
+            tile(v1s, kt + 1, n2);
+            __builtin_amdgcn_s_waitcnt(0);
+            lds_barrier();
+        }
     }
-    // O^T accumulator: lane holds d = 16db + 4(lane/16) + r for row my_row.
-    if (my_row >= seq) return;
-    if (k_tiles <= kChunkTiles) {
-        const float inv = 1.0f / l_run;
-        float* dst = out_rows + my_row * kHidden + h * kHeadDim;
+
+    // O^T accumulator: lane holds dims 2 (8 (r / 4) + 4 half + r % 4) + db of query my_q.
+    if (my_q >= seq) return;
+    const bool single = attn_chunks(seq, qt) == 1;
+    const float inv = single ? 1.0f / l_run : 1.0f;
+    float* dst = single ? out_rows + my_q * kHidden + h * kHeadDim
+                        : workspace + (attn_partial_slot(seq, qt, h, chunk) * kQTile + (my_q - qt * kQTile)) * kPartialRow;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) dst[16 * db + 4 * (lane >> 4) + r] = o_acc[db][r] * inv;
-        }
-    } else {
-        float* dst = workspace + (attn_partial_slot(seq, qt, h, chunk) * kQTile + (my_row - q0)) * kPartialRow;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) dst[16 * db + 4 * (lane >> 4) + r] = o_acc[db][r];
-        }
-        if (lane < 16) {
-            dst[kHeadDim] = m_run;  // log2 units
-            dst[kHeadDim + 1] = l_run;
-        }
+    for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * half + (r & 3);
+        dst[2 * i] = o_acc[0][r] * inv;
+        dst[2 * i + 1] = o_acc[1][r] * inv;
+    }
+    if (!single && half == 0) {
+        dst[kHeadDim] = m_run;  // log2 units
+        dst[kHeadDim + 1] = l_run;
     }
 }
 
 // Combines the chunk partials of query tiles with more than one chunk.  Block
-// ((qt - kChunkTiles) * 9 + h) * 16 + row group; thread t -> row 4 * group + t / 64,
+// ((qt - kLongTile) * 9 + h) * 32 + row group; thread t -> row 4 * group + t / 64,
 // dim t % 64.  All chunk loads of a thread are issued before the combine.
-constexpr int kMergeMaxChunks = 8;  // kMaxCapacity / (kChunkTiles * kKTile)
-
 __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(const float* __restrict__ workspace,
                                                                                int64_t seq,
                                                                                float* __restrict__ out_rows) {
     const int64_t tile_head = blockIdx.x / (kQTile / 4);
-    const int64_t qt = kChunkTiles + tile_head / kQHeads;
+    const int64_t qt = kLongTile + tile_head / kQHeads;
     const int h = static_cast<int>(tile_head % kQHeads);
     const int row = static_cast<int>(blockIdx.x % (kQTile / 4)) * 4 + static_cast<int>(threadIdx.x >> 6);
     const int d = threadIdx.x & 63;
     const int64_t q0 = qt * kQTile;
     if (q0 + row >= seq) return;
-    const int64_t last_key = q0 + kQTile - 1 < seq - 1 ? q0 + kQTile - 1 : seq - 1;
-    const int chunks = static_cast<int>((last_key / kKTile + kChunkTiles) / kChunkTiles);
+    const int chunks = static_cast<int>(attn_chunks(seq, qt));
     float o[kMergeMaxChunks], m[kMergeMaxChunks], l[kMergeMaxChunks];
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
@@ -456,7 +599,7 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(c
     float O = 0.0f, L = 0.0f;
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
-        const float f = m[c] == -INFINITY ? 0.0f : fast_exp2(m[c] - M);
+        const float f = fast_exp2(m[c] - M);
         O = fmaf(o[c], f, O);
         L = fmaf(l[c], f, L);
     }
@@ -514,8 +657,8 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
 }
 
 size_t prefill_attention_workspace_floats(int64_t seq) {
-    const int64_t long_tiles = attn_q_tiles(seq) - kChunkTiles;
-    if (long_tiles <= 0) return 0;
+    const int64_t long_tiles = attn_q_tiles(seq) - kLongTile;
+    if (long_tiles <= 0 || attn_max_chunks(seq) <= 1) return 0;
     return static_cast<size_t>(long_tiles * kQHeads * attn_max_chunks(seq) * kQTile * kPartialRow);
 }
 
@@ -525,14 +668,13 @@ hipError_t launch_prefill_attention(const float* q, const float* key_cache, cons
     if (seq <= 0 || seq > capacity) return hipErrorInvalidValue;
     if (prefill_attention_workspace_floats(seq) > 0 && workspace == nullptr) return hipErrorInvalidValue;
     if (attn_max_chunks(seq) > kMergeMaxChunks) return hipErrorInvalidValue;
-    int64_t blocks = 0;
-    for (int64_t c = 0; c < attn_max_chunks(seq); ++c) blocks += attn_chunk_blocks(seq, c);
+    const int64_t blocks = attn_items(seq) * kQHeads;
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kAttnThreads), 0, stream, q,
                        key_cache, value_cache, seq, capacity, scale, workspace, out_rows);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    const int64_t long_tiles = attn_q_tiles(seq) - kChunkTiles;
-    if (long_tiles > 0) {
+    const int64_t long_tiles = attn_q_tiles(seq) - kLongTile;
+    if (long_tiles > 0 && attn_max_chunks(seq) > 1) {
         hipLaunchKernelGGL(prefill_attention_merge_kernel,
                            dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / 4))), dim3(kAttnThreads), 0,
                            stream, workspace, seq, out_rows);

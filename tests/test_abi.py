@@ -83,11 +83,14 @@ def test_shape_constraints_are_rejected():
     assert lib.flux_gqa_decode_workspace_bytes(16385, ctypes.byref(size)) == _native.FLUX_ERROR_INVALID_VALUE
     assert lib.flux_gqa_decode_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 85 * 3 * 3 * 66 * 4
-    assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
+    # Keys are split into 1536-key chunks: up to 1536 tokens no 128-query tile sees two.
+    assert lib.flux_prefill_attention_workspace_bytes(1536, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 0
+    assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
+    # 4 query tiles past the first 12 x 9 heads x 2 chunks x 128 rows x (64 + m + l) floats
+    assert size.value == 4 * 9 * 2 * 128 * 66 * 4
     assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
-    # 96 query tiles past the first chunk x 9 heads x 4 chunks x 64 rows x (64 + m + l) floats
-    assert size.value == 96 * 9 * 4 * 64 * 66 * 4
+    assert size.value == 52 * 9 * 6 * 128 * 66 * 4
     dummy = ctypes.c_void_p(16)
     assert lib.flux_prefill_attention_f32(dummy, dummy, dummy, 4096, 4096, 0.125, None, dummy,
                                           None) == _native.FLUX_ERROR_INVALID_VALUE

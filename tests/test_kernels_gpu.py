@@ -306,9 +306,10 @@ def _attention_workspace(seq, device):
 
 
 @pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024),
-                                          (2049, 2100), (4160, 4160)])
+                                          (1537, 1600), (2049, 2100), (3201, 3300), (4160, 4160)])
 def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
-    # 2049 and 4160 exercise the split-key path (query tiles past 2048 keys) and its merge.
+    # From 1537 tokens on, query tiles see more than one 1536-key chunk: they take the
+    # split-key path and its merge (3201: three chunks and a one-query last tile).
     q = _randn(9, seq, D, seed=91).to(gpu_device)
     kc = _randn(3, capacity, D, seed=92).to(gpu_device)
     vc = _randn(3, capacity, D, seed=93).to(gpu_device)
