@@ -388,6 +388,11 @@ int flux_prefill_attention_f32(const float* q, const float* key_cache, const flo
     if (flux::prefill_attention_workspace_floats(seq) > 0 && !workspace)
         return invalid("flux_prefill_attention_f32: this prompt length needs a workspace "
                        "(flux_prefill_attention_workspace_bytes)");
+    for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(key_cache),
+                          static_cast<const void*>(value_cache), static_cast<const void*>(out_rows),
+                          static_cast<const void*>(workspace)})
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+            return invalid("flux_prefill_attention_f32: pointers must be 16-byte aligned");
     return from_hip(
         flux::launch_prefill_attention(q, key_cache, value_cache, seq, capacity, scale, workspace, out_rows, stream),
         "flux_prefill_attention_f32");

@@ -354,7 +354,7 @@ constexpr int kQTile = 128;
 constexpr int kKTile = 64;
 constexpr int kAttnThreads = 256;
 constexpr int kChunkTiles = 24;
-constexpr int kPartialRow = kHeadDim + 2;  // o[64], m, l
+constexpr int kPartialRow = kHeadDim + 4;  // o[64], m, l, 2 words of padding (16-byte rows)
 constexpr int kMergeMaxChunks = 16;        // kMaxCapacity / (kChunkTiles * kKTile)
 constexpr int kKVTileFloats = kKTile * kHeadDim;
 
@@ -661,39 +661,39 @@ prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ 
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int i = 8 * (r >> 2) + 4 * half + (r & 3);
-        dst[2 * i] = o_acc[0][r] * inv;
-        dst[2 * i + 1] = o_acc[1][r] * inv;
+        *reinterpret_cast<float2*>(dst + 2 * i) = make_float2(o_acc[0][r] * inv, o_acc[1][r] * inv);
     }
-    if (!single && half == 0) {
-        dst[kHeadDim] = m_run;  // log2 units
-        dst[kHeadDim + 1] = l_run;
-    }
+    if (!single && half == 0) *reinterpret_cast<float2*>(dst + kHeadDim) = make_float2(m_run, l_run);  // m in log2 units
 }
 
 // Combines the chunk partials of query tiles with more than one chunk.  Block
-// ((qt - kLongTile) * 9 + h) * 32 + row group; thread t -> row 4 * group + t / 64,
-// dim t % 64.  All chunk loads of a thread are issued before the combine.
+// ((qt - kLongTile) * 9 + h) * 8 + row group; thread t -> row 16 * group + t / 16,
+// dims 4 (t % 16) .. + 3.  All chunk loads of a thread are issued before the combine.
 __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(const float* __restrict__ workspace,
                                                                                int64_t seq,
                                                                                float* __restrict__ out_rows) {
-    const int64_t tile_head = blockIdx.x / (kQTile / 4);
+    constexpr int kRowsPerBlock = kAttnThreads / 16;
+    const int64_t tile_head = blockIdx.x / (kQTile / kRowsPerBlock);
     const int64_t qt = kLongTile + tile_head / kQHeads;
     const int h = static_cast<int>(tile_head % kQHeads);
-    const int row = static_cast<int>(blockIdx.x % (kQTile / 4)) * 4 + static_cast<int>(threadIdx.x >> 6);
-    const int d = threadIdx.x & 63;
+    const int row = static_cast<int>(blockIdx.x % (kQTile / kRowsPerBlock)) * kRowsPerBlock +
+                    static_cast<int>(threadIdx.x >> 4);
+    const int d = 4 * static_cast<int>(threadIdx.x & 15);
     const int64_t q0 = qt * kQTile;
     if (q0 + row >= seq) return;
     const int chunks = static_cast<int>(attn_chunks(seq, qt));
-    float o[kMergeMaxChunks], m[kMergeMaxChunks], l[kMergeMaxChunks];
+    float4 o[kMergeMaxChunks];
+    float m[kMergeMaxChunks], l[kMergeMaxChunks];
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
         if (c < chunks) {
             const float* p = workspace + (attn_partial_slot(seq, qt, h, c) * kQTile + row) * kPartialRow;
-            o[c] = p[d];
-            m[c] = p[kHeadDim];
-            l[c] = p[kHeadDim + 1];
+            o[c] = *reinterpret_cast<const float4*>(p + d);
+            const float2 ml = *reinterpret_cast<const float2*>(p + kHeadDim);
+            m[c] = ml.x;
+            l[c] = ml.y;
         } else {
-            o[c] = 0.0f;
+            o[c] = make_float4(0.f, 0.f, 0.f, 0.f);
             m[c] = -INFINITY;
             l[c] = 0.0f;
         }
@@ -701,14 +701,19 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(c
     float M = -INFINITY;
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) M = fmaxf(M, m[c]);
-    float O = 0.0f, L = 0.0f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.0f;
 #pragma unroll
     for (int c = 0; c < kMergeMaxChunks; ++c) {
         const float f = fast_exp2(m[c] - M);
-        O = fmaf(o[c], f, O);
+        O.x = fmaf(o[c].x, f, O.x);
+        O.y = fmaf(o[c].y, f, O.y);
+        O.z = fmaf(o[c].z, f, O.z);
+        O.w = fmaf(o[c].w, f, O.w);
         L = fmaf(l[c], f, L);
     }
-    out_rows[(q0 + row) * kHidden + h * kHeadDim + d] = O / L;
+    *reinterpret_cast<float4*>(out_rows + (q0 + row) * kHidden + h * kHeadDim + d) =
+        make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
 }
 
 __global__ void embedding_gather_kernel(const int64_t* ids, const float* embedding, int64_t vocab, int64_t seq,
@@ -792,8 +797,8 @@ hipError_t launch_prefill_attention(const float* q, const float* key_cache, cons
     const int64_t long_tiles = attn_q_tiles(seq) - kLongTile;
     if (long_tiles > 0 && attn_max_chunks(seq) > 1) {
         hipLaunchKernelGGL(prefill_attention_merge_kernel,
-                           dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / 4))), dim3(kAttnThreads), 0,
-                           stream, workspace, seq, out_rows);
+                           dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / (kAttnThreads / 16)))),
+                           dim3(kAttnThreads), 0, stream, workspace, seq, out_rows);
         st = hipGetLastError();
     }
     return st;

@@ -87,14 +87,17 @@ def test_shape_constraints_are_rejected():
     assert lib.flux_prefill_attention_workspace_bytes(1536, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 0
     assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
-    # 4 query tiles past the first 12 x 9 heads x 2 chunks x 128 rows x (64 + m + l) floats
-    assert size.value == 4 * 9 * 2 * 128 * 66 * 4
+    # 4 query tiles past the first 12 x 9 heads x 2 chunks x 128 rows x (64 + m + l + 2 pad) floats
+    assert size.value == 4 * 9 * 2 * 128 * 68 * 4
     assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
-    assert size.value == 52 * 9 * 6 * 128 * 66 * 4
+    assert size.value == 52 * 9 * 6 * 128 * 68 * 4
     dummy = ctypes.c_void_p(16)
     assert lib.flux_prefill_attention_f32(dummy, dummy, dummy, 4096, 4096, 0.125, None, dummy,
                                           None) == _native.FLUX_ERROR_INVALID_VALUE
     assert "workspace" in _native.last_error()
+    assert lib.flux_prefill_attention_f32(dummy, dummy, dummy, 64, 64, 0.125, None, ctypes.c_void_p(20),
+                                          None) == _native.FLUX_ERROR_INVALID_VALUE
+    assert "16-byte aligned" in _native.last_error()
 
 
 def test_runtime_constructor_validation_messages():
