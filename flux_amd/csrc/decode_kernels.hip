@@ -1028,7 +1028,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             const int64_t per = (args.vocab + TW - 1) / TW;
             const int64_t row0 = per * gw < args.vocab ? per * gw : args.vocab;
             const int64_t row1 = row0 + per < args.vocab ? row0 + per : args.vocab;
-            const int layer = kLayers;
+            [[maybe_unused]] const int layer = kLayers;  // read by the trace points
             FLUX_TRACE_POINT(0);
             // The first kLmBatch rows of this wave are loaded before waiting for h.
             float wl[kLmBatch][9];

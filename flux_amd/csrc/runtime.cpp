@@ -133,7 +133,7 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
                              int64_t capacity, int64_t position, const int64_t* initial_token,
                              const CacheSources& sources, const double* epsilons, const double* scales,
                              hipStream_t stream)
-    : capacity_(capacity), start_position_(position), weights_(weights), rope_cos_(rope_cos), rope_sin_(rope_sin) {
+    : capacity_(capacity), start_position_(position), rope_cos_(rope_cos), rope_sin_(rope_sin) {
     validate_weights(weights, "flux native full decode");
     validate_scalars(epsilons, scales, "flux native full decode");
     if (capacity < 1 || capacity > kMaxCapacity)

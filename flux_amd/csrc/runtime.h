@@ -75,7 +75,6 @@ private:
     bool pending_ = false;
     bool generation_started_ = false;
 
-    flux_weights weights_{};
     const float* rope_cos_ = nullptr;
     const float* rope_sin_ = nullptr;
     float final_eps_ = 0.0f;
