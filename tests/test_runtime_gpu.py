@@ -12,7 +12,9 @@ import numpy as np
 import pytest
 import torch
 
+from flux_amd import synthetic
 from flux_amd.runtime import NativeSmolLM2Decode, NativeSmolLM2Prefill, native_smollm2_greedy_generate
+from oracle.llama_fp32 import OracleCache, OracleLlama, top2_margin
 from tests.conftest import golden
 
 pytestmark = pytest.mark.gpu
@@ -188,3 +190,28 @@ def test_end_to_end_8192_plus_512_is_deterministic(smol_model):
     assert torch.equal(first, second)
     assert torch.equal(logits_first, runtime.logits)
     assert runtime.device_error() == 0
+
+
+@pytest.mark.parametrize("length", [1537, 3001])
+def test_odd_length_prefill_matches_oracle(small_model, length):
+    """Prompt lengths that end inside a 128-query attention tile and split the keys of the
+    later tiles into 1536-key chunks (3001: three chunks), through the whole native
+    prefill, against the CPU oracle: last-row logits, greedy token, K/V cache rows."""
+    g = torch.Generator().manual_seed(length)
+    prompt = torch.randint(0, 128, (1, length), generator=g)
+    runtime = NativeSmolLM2Prefill.capture(small_model, prompt.cuda(), max_decode_steps=1)
+    torch.cuda.synchronize()
+    oracle = OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128)))
+    cache = OracleCache()
+    with torch.inference_mode():
+        expected = oracle.forward(prompt, cache)[0, -1]
+    logits = runtime.logits[0, 0].float().cpu()
+    torch.testing.assert_close(logits, expected, atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
+    if top2_margin(expected) > 1e-3:
+        assert int(runtime.current_token.item()) == int(torch.argmax(expected))
+    positions = torch.tensor([0, 1535, 1536, length - 2, length - 1])
+    for layer in (0, 29):
+        k = runtime.key_cache[layer, 0][:, positions].float().cpu()
+        v = runtime.value_cache[layer, 0][:, positions].float().cpu()
+        torch.testing.assert_close(k, cache.keys[layer][0][:, positions], rtol=KV_RTOL, atol=KV_ATOL)
+        torch.testing.assert_close(v, cache.values[layer][0][:, positions], rtol=KV_RTOL, atol=KV_ATOL)
