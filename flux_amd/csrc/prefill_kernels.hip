@@ -161,14 +161,28 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 2; ++q) bv[j][q] = *reinterpret_cast<const f32x4*>(&b_s[buf][b_off[j][q]]);
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
+        if constexpr (E == GemmEpilogue::kSwiglu) {
+            // Written accumulator by accumulator: the compiler then schedules the stage's
+            // operand reads and barrier ahead of its MFMAs, which measured 4% faster for
+            // this shape (and slower for the others).
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3], bv[j][kk >> 2][kk & 3],
-                                                                   acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3],
+                                                                       bv[j][kk >> 2][kk & 3], acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3],
+                                                                       bv[j][kk >> 2][kk & 3], acc[i][j], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);  // next stage's tiles have landed in LDS
         __syncthreads();
