@@ -325,14 +325,18 @@ def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
     _close(out.view(seq, 9, D).transpose(0, 1), expected, rtol=2e-4, atol=2e-5)
 
 
-def test_prefill_attention_zero_query_prefix_mean(gpu_device):
-    seq, capacity = 130, 130
+@pytest.mark.parametrize("seq", [130, 16384])
+def test_prefill_attention_zero_query_prefix_mean(gpu_device, seq):
+    # Zero queries make every visible key equally likely, so row s is the mean of V[0..s]:
+    # a closed form that pins the split-key merge at the largest capacity too.
+    capacity = seq
     q = torch.zeros(9, seq, D, device=gpu_device)
     kc = _randn(3, capacity, D, seed=94).to(gpu_device)
     vc = _randn(3, capacity, D, seed=95).to(gpu_device)
     out = torch.empty(seq, H, device=gpu_device)
+    ws = _attention_workspace(seq, gpu_device)
     _native.check(_lib().flux_prefill_attention_f32(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), seq, capacity, 0.125,
-                                                    None, out.data_ptr(), _s(gpu_device)))
+                                                    ws.data_ptr(), out.data_ptr(), _s(gpu_device)))
     torch.cuda.synchronize()
     prefix = vc.cpu().double().cumsum(dim=1) / torch.arange(1, capacity + 1).double()[None, :, None]
     expected = prefix[:, :seq].repeat_interleave(3, dim=0)
