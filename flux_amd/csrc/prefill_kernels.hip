@@ -75,6 +75,56 @@ __device__ __forceinline__ void lds_copy16(const float* src, float* lds) {
     __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
 }
 
+// Epilogue of one wave's (32*MI) x 64 tile whose first row is row0 and whose column
+// group (one head for RoPE, one gate/up pair for SwiGLU) starts at column g0.
+template <GemmEpilogue E, int MI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const f32x16 (&acc)[MI][2], int64_t row0, int g0,
+                                              int lane) {
+    // Epilogue: for 32-row subtile i, lane holds columns c (acc[i][0]) and c + 32
+    // (acc[i][1]) of the wave's 64-column group for 16 rows.
+    const int j = lane & 31;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = row0 + 32 * i + mfma32_row(lane, r);
+            if (row >= args.m) continue;
+            const float lo = acc[i][0][r];
+            const float hi = acc[i][1][r];
+            if constexpr (E == GemmEpilogue::kStore) {
+                args.c[row * args.n + g0 + j] = lo;
+                args.c[row * args.n + g0 + 32 + j] = hi;
+            } else if constexpr (E == GemmEpilogue::kResidual) {
+                const int64_t i0 = row * args.n + g0 + j;
+                args.c[i0] = args.residual[i0] + lo;
+                args.c[i0 + 32] = args.residual[i0 + 32] + hi;
+            } else if constexpr (E == GemmEpilogue::kSwiglu) {
+                const int half = args.n / 2;
+                args.c[row * half + (g0 >> 1) + j] = silu(lo) * hi;
+            } else {  // kQkvRope: the column group is one head; columns j / j+32 are the RoPE pair.
+                const int head = g0 / kHeadDim;
+                if (head < kQHeads + kKVHeads) {
+                    const float* cr = args.rope_cos + row * kHeadDim;
+                    const float* sr = args.rope_sin + row * kHeadDim;
+                    const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
+                    const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
+                    float* dst = head < kQHeads
+                                     ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
+                                     : args.key_cache +
+                                           (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
+                    dst[j] = qlo;
+                    dst[j + 32] = qhi;
+                } else {
+                    float* dst = args.value_cache +
+                                 (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
+                    dst[j] = lo;
+                    dst[j + 32] = hi;
+                }
+            }
+        }
+    }
+}
+
 // C = epilogue(A[M,K] * W[N,K]^T) on v_mfma_f32_32x32x2f32.  Block tile (64*MI) x 128,
 // 4 waves in 2 x 2, wave tile (32*MI) x 64.  K is consumed 16 at a time; MFMA
 // instruction s (0..7) of a stage pairs K index s (lanes 0-31) with s + 8 (lanes
@@ -188,51 +238,155 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
         __syncthreads();
     }
     if (!group_valid) return;
+    gemm_epilogue<E, MI>(args, acc, m0 + wm * 32 * MI, n0 + wn * 64, lane);
+}
 
-    // Epilogue: for 32-row subtile i, lane holds columns c (acc[i][0]) and c + 32
-    // (acc[i][1]) of the wave's 64-column group for 16 rows.
-    const int j = lane & 31;
-    const int g0 = n0 + wn * 64;  // first column of the group
+// Waits until at most N vector-memory operations of this wave are outstanding
+// (vmcnt only; the LDS and export counters are left alone).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Barrier for LDS hand-offs: this wave's LDS reads are complete and no memory access
+// moves across it; global-memory copies still in flight are not waited for (each
+// wave waits for its own with vmcnt where needed).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// gemm_kernel for grids smaller than the device (short prompts): with one block per
+// CU or fewer nothing hides a block's copy latency, so stages stream through a ring
+// of four buffers, three copies in flight (each buffer its own LDS variable so reads
+// of one never wait on copies into another).  Step s reads stage s, starts the copy
+// of stage s + 3 into the buffer stage s - 1 used, multiplies, then waits for stage
+// s + 1.  The step count is rounded up to a multiple of 4 and copies past the last
+// stage repeat it, so every step issues and waits alike; surplus steps skip the MFMAs.
+template <GemmEpilogue E, int MI>
+__global__ void __launch_bounds__(kGemmThreads) gemm_ring_kernel(GemmArgs args) {
+    constexpr int kNS = 4;
+    constexpr int kBMt = 64 * MI;
+    __shared__ __align__(16) float a_s0[kBMt * kBK];
+    __shared__ __align__(16) float a_s1[kBMt * kBK];
+    __shared__ __align__(16) float a_s2[kBMt * kBK];
+    __shared__ __align__(16) float a_s3[kBMt * kBK];
+    __shared__ __align__(16) float b_s0[kBN * kBK];
+    __shared__ __align__(16) float b_s1[kBN * kBK];
+    __shared__ __align__(16) float b_s2[kBN * kBK];
+    __shared__ __align__(16) float b_s3[kBN * kBK];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBMt;
+    const int n0 = blockIdx.x * kBN;
+    const int K = args.k;
+    const bool group_valid = n0 + wn * 64 < args.n;
+
+    constexpr int kAPerWave = kBMt / 64;
+    constexpr int kLoads = kAPerWave + 2;  // global_load_lds per wave per stage
+    const float* a_src[kAPerWave];
+    const float* b_src[2];
+#pragma unroll
+    for (int j = 0; j < kAPerWave; ++j) {
+        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+        const int64_t gr = m0 + row < args.m ? m0 + row : args.m - 1;
+        a_src[j] = args.a + gr * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+        const int col = n0 + row < args.n ? n0 + row : args.n - 1;
+        b_src[j] = args.b + static_cast<int64_t>(b_row<E>(col, args.n)) * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
+    }
+    auto abuf = [&](auto bi) -> float* {
+        constexpr int b = decltype(bi)::value;
+        if constexpr (b == 0) return a_s0;
+        else if constexpr (b == 1) return a_s1;
+        else if constexpr (b == 2) return a_s2;
+        else return a_s3;
+    };
+    auto bbuf = [&](auto bi) -> float* {
+        constexpr int b = decltype(bi)::value;
+        if constexpr (b == 0) return b_s0;
+        else if constexpr (b == 1) return b_s1;
+        else if constexpr (b == 2) return b_s2;
+        else return b_s3;
+    };
+    const int stages = K / kBK;
+    auto issue = [&](auto bi, int st) {
+        const int k0 = (st < stages ? st : stages - 1) * kBK;
+        float* as = abuf(bi);
+        float* bs = bbuf(bi);
+#pragma unroll
+        for (int j = 0; j < kAPerWave; ++j) lds_copy16(a_src[j] + k0, as + (wave + 4 * j) * 16 * kBK);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) lds_copy16(b_src[j] + k0, bs + (wave + 4 * j) * 16 * kBK);
+    };
+
+    f32x16 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int h = lane >> 5;
+    int a_off[MI][2], b_off[2][2];
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wm * 32 * MI + 32 * i + mfma32_row(lane, r);
-            if (row >= args.m) continue;
-            const float lo = acc[i][0][r];
-            const float hi = acc[i][1][r];
-            if constexpr (E == GemmEpilogue::kStore) {
-                args.c[row * args.n + g0 + j] = lo;
-                args.c[row * args.n + g0 + 32 + j] = hi;
-            } else if constexpr (E == GemmEpilogue::kResidual) {
-                const int64_t i0 = row * args.n + g0 + j;
-                args.c[i0] = args.residual[i0] + lo;
-                args.c[i0 + 32] = args.residual[i0 + 32] + hi;
-            } else if constexpr (E == GemmEpilogue::kSwiglu) {
-                const int half = args.n / 2;
-                args.c[row * half + (g0 >> 1) + j] = silu(lo) * hi;
-            } else {  // kQkvRope: the column group is one head; columns j / j+32 are the RoPE pair.
-                const int head = g0 / kHeadDim;
-                if (head < kQHeads + kKVHeads) {
-                    const float* cr = args.rope_cos + row * kHeadDim;
-                    const float* sr = args.rope_sin + row * kHeadDim;
-                    const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
-                    const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
-                    float* dst = head < kQHeads
-                                     ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
-                                     : args.key_cache +
-                                           (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
-                    dst[j] = qlo;
-                    dst[j + 32] = qhi;
-                } else {
-                    float* dst = args.value_cache +
-                                 (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
-                    dst[j] = lo;
-                    dst[j + 32] = hi;
-                }
-            }
-        }
+        const int r = wm * 32 * MI + 32 * i + (lane & 31);
+        a_off[i][0] = tile_offset(r, 2 * h);
+        a_off[i][1] = tile_offset(r, 2 * h + 1);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + 32 * j + (lane & 31);
+        b_off[j][0] = tile_offset(r, 2 * h);
+        b_off[j][1] = tile_offset(r, 2 * h + 1);
+    }
+
+    auto step = [&](auto bi, int s) {
+        constexpr int b = decltype(bi)::value;
+        const float* as = abuf(bi);
+        const float* bs = bbuf(bi);
+        f32x4 av[MI][2], bv[2][2];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) av[i][q] = *reinterpret_cast<const f32x4*>(as + a_off[i][q]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) bv[j][q] = *reinterpret_cast<const f32x4*>(bs + b_off[j][q]);
+        issue(std::integral_constant<int, (b + kNS - 1) % kNS>{}, s + kNS - 1);
+        if (s < stages) {
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3],
+                                                                       bv[j][kk >> 2][kk & 3], acc[i][j], 0, 0, 0);
+        }
+        wait_vmcnt<(kNS - 2) * kLoads>();
+        lds_barrier();
+    };
+    issue(std::integral_constant<int, 0>{}, 0);
+    issue(std::integral_constant<int, 1>{}, 1);
+    issue(std::integral_constant<int, 2>{}, 2);
+    wait_vmcnt<(kNS - 2) * kLoads>();
+    lds_barrier();
+    for (int s = 0; s < stages; s += kNS) {
+        step(std::integral_constant<int, 0>{}, s);
+        step(std::integral_constant<int, 1>{}, s + 1);
+        step(std::integral_constant<int, 2>{}, s + 2);
+        step(std::integral_constant<int, 3>{}, s + 3);
+    }
+    wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
+    if (!group_valid) return;
+    gemm_epilogue<E, MI>(args, acc, m0 + wm * 32 * MI, n0 + wn * 64, lane);
 }
 
 // Narrow-column variant for the residual / plain epilogues of N = 576 outputs
@@ -325,6 +479,131 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
             __syncthreads();
         }
     }
+
+    const int col = n0 + wn * 32 + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 32 + mfma32_row(lane, r);
+        if (row >= args.m) continue;
+        const int64_t i0 = row * args.n + col;
+        if constexpr (E == GemmEpilogue::kResidual) {
+            args.c[i0] = args.residual[i0] + acc[r];
+        } else {
+            args.c[i0] = acc[r];
+        }
+    }
+}
+
+// gemm_narrow_kernel for grids smaller than the device: the same 64 x 64 tiles and
+// 32-deep stages through a ring of four buffers (three copies in flight), stepped as
+// in gemm_ring_kernel.
+template <GemmEpilogue E>
+__global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs args) {
+    static_assert(E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual, "plain epilogues only");
+    constexpr int kNS = 4;
+    constexpr int kRows = 64;
+    constexpr int kDepth = 32;
+    constexpr int kLoads = 4;  // global_load_lds per wave per stage
+    __shared__ __align__(16) float a_s0[kRows * kDepth];
+    __shared__ __align__(16) float a_s1[kRows * kDepth];
+    __shared__ __align__(16) float a_s2[kRows * kDepth];
+    __shared__ __align__(16) float a_s3[kRows * kDepth];
+    __shared__ __align__(16) float b_s0[kRows * kDepth];
+    __shared__ __align__(16) float b_s1[kRows * kDepth];
+    __shared__ __align__(16) float b_s2[kRows * kDepth];
+    __shared__ __align__(16) float b_s3[kRows * kDepth];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kRows;
+    const int n0 = blockIdx.x * kRows;
+    const int K = args.k;
+
+    const float* a_src[2];
+    const float* b_src[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 8 * (wave + 4 * j) + (lane >> 3);
+        const int piece = (lane & 7) ^ ((row >> 1) & 7);
+        const int64_t ga = m0 + row < args.m ? m0 + row : args.m - 1;
+        a_src[j] = args.a + ga * K + 4 * piece;
+        b_src[j] = args.b + static_cast<int64_t>(n0 + row) * K + 4 * piece;
+    }
+    auto abuf = [&](auto bi) -> float* {
+        constexpr int b = decltype(bi)::value;
+        if constexpr (b == 0) return a_s0;
+        else if constexpr (b == 1) return a_s1;
+        else if constexpr (b == 2) return a_s2;
+        else return a_s3;
+    };
+    auto bbuf = [&](auto bi) -> float* {
+        constexpr int b = decltype(bi)::value;
+        if constexpr (b == 0) return b_s0;
+        else if constexpr (b == 1) return b_s1;
+        else if constexpr (b == 2) return b_s2;
+        else return b_s3;
+    };
+    const int stages = K / kDepth;
+    auto issue = [&](auto bi, int st) {
+        const int k0 = (st < stages ? st : stages - 1) * kDepth;
+        float* as = abuf(bi);
+        float* bs = bbuf(bi);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            lds_copy16(a_src[j] + k0, as + (wave + 4 * j) * 8 * kDepth);
+            lds_copy16(b_src[j] + k0, bs + (wave + 4 * j) * 8 * kDepth);
+        }
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int h = lane >> 5;
+    const int ra = wm * 32 + (lane & 31);
+    const int rb = wn * 32 + (lane & 31);
+    int a_off[4], b_off[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            a_off[2 * u + q] = ra * kDepth + 4 * ((4 * u + 2 * h + q) ^ ((ra >> 1) & 7));
+            b_off[2 * u + q] = rb * kDepth + 4 * ((4 * u + 2 * h + q) ^ ((rb >> 1) & 7));
+        }
+    auto step = [&](auto bi, int s) {
+        constexpr int b = decltype(bi)::value;
+        const float* as = abuf(bi);
+        const float* bs = bbuf(bi);
+        f32x4 av[4], bv[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            av[p] = *reinterpret_cast<const f32x4*>(as + a_off[p]);
+            bv[p] = *reinterpret_cast<const f32x4*>(bs + b_off[p]);
+        }
+        issue(std::integral_constant<int, (b + kNS - 1) % kNS>{}, s + kNS - 1);
+        if (s < stages) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p][kk], bv[p][kk], acc, 0, 0, 0);
+        }
+        wait_vmcnt<(kNS - 2) * kLoads>();
+        lds_barrier();
+    };
+    issue(std::integral_constant<int, 0>{}, 0);
+    issue(std::integral_constant<int, 1>{}, 1);
+    issue(std::integral_constant<int, 2>{}, 2);
+    wait_vmcnt<(kNS - 2) * kLoads>();
+    lds_barrier();
+    for (int s = 0; s < stages; s += kNS) {
+        step(std::integral_constant<int, 0>{}, s);
+        step(std::integral_constant<int, 1>{}, s + 1);
+        step(std::integral_constant<int, 2>{}, s + 2);
+        step(std::integral_constant<int, 3>{}, s + 3);
+    }
+    wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
 
     const int col = n0 + wn * 32 + (lane & 31);
 #pragma unroll
@@ -451,10 +730,6 @@ __device__ __forceinline__ float halves_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Workgroup barrier for LDS hand-offs: this wave's LDS reads are complete and no
-// memory access moves across it; global-memory copies still in flight are not
-// waited for (each wave waits for its own with vmcnt where needed).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(3)))
 prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ key_cache,
@@ -746,6 +1021,9 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 
 }  // namespace
 
+// Grids below this many blocks (fewer than the device's CUs) use the ring kernels.
+constexpr int64_t kRingBlocks = 256;
+
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
@@ -755,21 +1033,36 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         args.k % 32 == 0) {
         // Column counts that are not a multiple of 128 (576): 64 x 64 tiles.
         const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
-        if (epilogue == GemmEpilogue::kResidual)
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kResidual>), grid, block, 0, stream,
-                               args);
-        else
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kStore>), grid, block, 0, stream, args);
+        const bool small = static_cast<int64_t>(grid.x) * grid.y < kRingBlocks;
+        if (epilogue == GemmEpilogue::kResidual) {
+            if (small)
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_ring_kernel<GemmEpilogue::kResidual>), grid, block, 0,
+                                   stream, args);
+            else
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kResidual>), grid, block, 0,
+                                   stream, args);
+        } else {
+            if (small)
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_ring_kernel<GemmEpilogue::kStore>), grid, block, 0,
+                                   stream, args);
+            else
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kStore>), grid, block, 0, stream,
+                                   args);
+        }
         return hipGetLastError();
     }
-    // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles.
+    // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles;
+    // grids smaller than the device take the copy ring.
     const unsigned gx = static_cast<unsigned>((args.n + kBN - 1) / kBN);
     const bool big = static_cast<int64_t>(gx) * ((args.m + 127) / 128) >= 512;
     const dim3 grid(gx, static_cast<unsigned>(big ? (args.m + 127) / 128 : (args.m + 63) / 64));
+    const bool small = static_cast<int64_t>(grid.x) * grid.y < kRingBlocks;
 #define FLUX_LAUNCH_GEMM(E)                                                                    \
     do {                                                                                       \
         if (big)                                                                               \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 2>), grid, block, 0, stream, args);             \
+        else if (small)                                                                        \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_ring_kernel<E, 1>), grid, block, 0, stream, args);        \
         else                                                                                   \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 1>), grid, block, 0, stream, args);             \
     } while (0)
