@@ -77,6 +77,40 @@ __device__ __forceinline__ void lds_copy16(const float* src, float* lds) {
 
 // Epilogue of one wave's (32*MI) x 64 tile whose first row is row0 and whose column
 // group (one head for RoPE, one gate/up pair for SwiGLU) starts at column g0.
+// One output row of a wave's 64-column group: lo is column g0 + j, hi is column g0 + 32 + j.
+template <GemmEpilogue E>
+__device__ __forceinline__ void gemm_store_pair(const GemmArgs& args, int64_t row, int g0, int j, float lo, float hi) {
+    if constexpr (E == GemmEpilogue::kStore) {
+        args.c[row * args.n + g0 + j] = lo;
+        args.c[row * args.n + g0 + 32 + j] = hi;
+    } else if constexpr (E == GemmEpilogue::kResidual) {
+        const int64_t i0 = row * args.n + g0 + j;
+        args.c[i0] = args.residual[i0] + lo;
+        args.c[i0 + 32] = args.residual[i0 + 32] + hi;
+    } else if constexpr (E == GemmEpilogue::kSwiglu) {
+        const int half = args.n / 2;
+        args.c[row * half + (g0 >> 1) + j] = silu(lo) * hi;
+    } else {  // kQkvRope: the column group is one head; columns j / j+32 are the RoPE pair.
+        const int head = g0 / kHeadDim;
+        if (head < kQHeads + kKVHeads) {
+            const float* cr = args.rope_cos + row * kHeadDim;
+            const float* sr = args.rope_sin + row * kHeadDim;
+            const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
+            const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
+            float* dst = head < kQHeads
+                             ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
+                             : args.key_cache + (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
+            dst[j] = qlo;
+            dst[j + 32] = qhi;
+        } else {
+            float* dst = args.value_cache +
+                         (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
+            dst[j] = lo;
+            dst[j + 32] = hi;
+        }
+    }
+}
+
 template <GemmEpilogue E, int MI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const f32x16 (&acc)[MI][2], int64_t row0, int g0,
                                               int lane) {
@@ -89,38 +123,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const f32x16
         for (int r = 0; r < 16; ++r) {
             const int64_t row = row0 + 32 * i + mfma32_row(lane, r);
             if (row >= args.m) continue;
-            const float lo = acc[i][0][r];
-            const float hi = acc[i][1][r];
-            if constexpr (E == GemmEpilogue::kStore) {
-                args.c[row * args.n + g0 + j] = lo;
-                args.c[row * args.n + g0 + 32 + j] = hi;
-            } else if constexpr (E == GemmEpilogue::kResidual) {
-                const int64_t i0 = row * args.n + g0 + j;
-                args.c[i0] = args.residual[i0] + lo;
-                args.c[i0 + 32] = args.residual[i0 + 32] + hi;
-            } else if constexpr (E == GemmEpilogue::kSwiglu) {
-                const int half = args.n / 2;
-                args.c[row * half + (g0 >> 1) + j] = silu(lo) * hi;
-            } else {  // kQkvRope: the column group is one head; columns j / j+32 are the RoPE pair.
-                const int head = g0 / kHeadDim;
-                if (head < kQHeads + kKVHeads) {
-                    const float* cr = args.rope_cos + row * kHeadDim;
-                    const float* sr = args.rope_sin + row * kHeadDim;
-                    const float qlo = rope_lo(lo, hi, cr[j], sr[j]);
-                    const float qhi = rope_hi(hi, lo, cr[j + 32], sr[j + 32]);
-                    float* dst = head < kQHeads
-                                     ? args.q_out + (static_cast<int64_t>(head) * args.m + row) * kHeadDim
-                                     : args.key_cache +
-                                           (static_cast<int64_t>(head - kQHeads) * args.capacity + row) * kHeadDim;
-                    dst[j] = qlo;
-                    dst[j + 32] = qhi;
-                } else {
-                    float* dst = args.value_cache +
-                                 (static_cast<int64_t>(head - kQHeads - kKVHeads) * args.capacity + row) * kHeadDim;
-                    dst[j] = lo;
-                    dst[j + 32] = hi;
-                }
-            }
+            gemm_store_pair<E>(args, row, g0, j, acc[i][0][r], acc[i][1][r]);
         }
     }
 }
@@ -491,6 +494,146 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
         } else {
             args.c[i0] = acc[r];
         }
+    }
+}
+
+// Few rows (short prompts): one block per 32 x 64 output tile, its kSplitWaves waves
+// splitting K into contiguous ranges.  A wave streams its range 16 K values at a time
+// (32 A rows and the tile's 64 B rows, 64 bytes each, laid out and swizzled as in
+// gemm_kernel) through a private ring of kSplitStages LDS buffers; while a stage's MFMAs run,
+// the next stage's operands are already in registers and the kSplitStages - 2 after it are
+// being copied.  No wave waits for another until the partial tiles meet in LDS.
+// They are summed in wave order (the result does not depend on timing), and wave w
+// then finishes accumulator registers 4w .. 4w + 3 through the shared epilogue.
+constexpr int kSplitWaves = 4;
+constexpr int kSplitStages = 5;
+constexpr int kSplitRows = 96;  // 32 A rows + 64 B rows per stage
+constexpr int kSplitCopies = kSplitRows / 16;
+
+template <int S, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (S < N) {
+        f(std::integral_constant<int, S>{});
+        static_for<S + 1, N>(f);
+    }
+}
+
+// kStages = K / (kSplitWaves * 16), fixed at compile time so the stage loop is straight-line
+// code and every wait names exactly the copies it needs.
+template <GemmEpilogue E, int kStages>
+__global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs args) {
+    static_assert(kSplitStages == 5, "the buffers below are spelled out");
+    // One variable per ring slot: a read of one slot then never waits for copies into another.
+    __shared__ __align__(16) float r0[kSplitWaves][kSplitRows * kBK];
+    __shared__ __align__(16) float r1[kSplitWaves][kSplitRows * kBK];
+    __shared__ __align__(16) float r2[kSplitWaves][kSplitRows * kBK];
+    __shared__ __align__(16) float r3[kSplitWaves][kSplitRows * kBK];
+    __shared__ __align__(16) float r4[kSplitWaves][kSplitRows * kBK];
+    __shared__ float partial[kSplitWaves][2][16][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32;
+    const int n0 = blockIdx.x * 64;
+    const int K = args.k;
+    constexpr int kSpan = kStages * kBK;  // this wave's K values start at wave * kSpan
+
+    const float* src[kSplitCopies];
+#pragma unroll
+    for (int i = 0; i < kSplitCopies; ++i) {
+        const int row = 16 * i + (lane >> 2);
+        const int piece = (lane & 3) ^ ((row >> 2) & 3);
+        const float* base;
+        if (row < 32) {
+            const int64_t ga = m0 + row < args.m ? m0 + row : args.m - 1;
+            base = args.a + ga * K;
+        } else {
+            base = args.b + static_cast<int64_t>(b_row<E>(n0 + row - 32, args.n)) * K;
+        }
+        src[i] = base + wave * kSpan + 4 * piece;
+    }
+    auto slot = [&](auto bi) -> float* {
+        constexpr int b = decltype(bi)::value % kSplitStages;
+        if constexpr (b == 0) return r0[wave];
+        else if constexpr (b == 1) return r1[wave];
+        else if constexpr (b == 2) return r2[wave];
+        else if constexpr (b == 3) return r3[wave];
+        else return r4[wave];
+    };
+    auto issue = [&](auto st) {
+        float* dst = slot(st);
+#pragma unroll
+        for (int i = 0; i < kSplitCopies; ++i) lds_copy16(src[i] + decltype(st)::value * kBK, dst + i * 16 * kBK);
+    };
+
+    const int h = lane >> 5;
+    const int ra = lane & 31;
+    const int a_off0 = tile_offset(ra, 2 * h), a_off1 = tile_offset(ra, 2 * h + 1);
+    const int b_off[2][2] = {{tile_offset(32 + ra, 2 * h), tile_offset(32 + ra, 2 * h + 1)},
+                             {tile_offset(64 + ra, 2 * h), tile_offset(64 + ra, 2 * h + 1)}};
+    f32x16 acc[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[0][r] = 0.0f;
+        acc[1][r] = 0.0f;
+    }
+    struct Operands {
+        f32x4 a[2];
+        f32x4 b[2][2];
+    };
+    auto read = [&](auto st, Operands& o) {
+        const float* t = slot(st);
+        o.a[0] = *reinterpret_cast<const f32x4*>(t + a_off0);
+        o.a[1] = *reinterpret_cast<const f32x4*>(t + a_off1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) o.b[j][q] = *reinterpret_cast<const f32x4*>(t + b_off[j][q]);
+    };
+    constexpr int kAhead = kSplitStages - 1;  // stages issued before the loop
+    static_for<0, (kStages < kAhead ? kStages : kAhead)>([&](auto st) { issue(st); });
+    Operands cur, nxt;
+    wait_vmcnt<((kStages < kAhead ? kStages : kAhead) - 1) * kSplitCopies>();
+    read(std::integral_constant<int, 0>{}, cur);
+    static_for<0, kStages>([&](auto st) {
+        constexpr int s = decltype(st)::value;
+        // Slot (s + kAhead) % kSplitStages last held stage s - 1, whose operands were read in
+        // step s - 2 and consumed in step s - 1.
+        if constexpr (s + 1 < kStages) {
+            constexpr int newest = s + kAhead - 1 < kStages ? s + kAhead - 1 : kStages - 1;
+            wait_vmcnt<(newest - s - 1) * kSplitCopies>();
+            read(std::integral_constant<int, s + 1>{}, nxt);
+        }
+        if constexpr (s + kAhead < kStages) issue(std::integral_constant<int, s + kAhead>{});
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[kk >> 2][kk & 3], cur.b[j][kk >> 2][kk & 3], acc[j],
+                                                              0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        cur = nxt;
+    });
+    wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        partial[wave][0][r][lane] = acc[0][r];
+        partial[wave][1][r][lane] = acc[1][r];
+    }
+    __syncthreads();
+    const int j = lane & 31;
+#pragma unroll
+    for (int u = 0; u < 16 / kSplitWaves; ++u) {
+        const int r = (16 / kSplitWaves) * wave + u;
+        float lo = partial[0][0][r][lane], hi = partial[0][1][r][lane];
+#pragma unroll
+        for (int w = 1; w < kSplitWaves; ++w) {
+            lo += partial[w][0][r][lane];
+            hi += partial[w][1][r][lane];
+        }
+        const int64_t out_row = m0 + mfma32_row(lane, r);
+        if (out_row < args.m) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
     }
 }
 
@@ -1023,11 +1166,41 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 
 // Grids below this many blocks (fewer than the device's CUs) use the ring kernels.
 constexpr int64_t kRingBlocks = 256;
+constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
+    const int split_stages = args.k % (kSplitWaves * kBK) == 0 ? args.k / (kSplitWaves * kBK) : 0;
+    if ((split_stages == 9 || split_stages == 24) && (args.n / 64) * ((args.m + 31) / 32) <= kSplitBlocks) {
+        // K = 576 (hidden) or 1536 (intermediate): one 32 x 64 tile per block.
+        const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 31) / 32));
+        const dim3 split_block(64 * kSplitWaves);
+#define FLUX_LAUNCH_SPLIT(E)                                                                                       \
+    do {                                                                                                           \
+        if (split_stages == 9)                                                                                     \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, 9>), grid, split_block, 0, stream, args);      \
+        else                                                                                                       \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, 24>), grid, split_block, 0, stream, args);     \
+    } while (0)
+        switch (epilogue) {
+            case GemmEpilogue::kStore:
+                FLUX_LAUNCH_SPLIT(GemmEpilogue::kStore);
+                break;
+            case GemmEpilogue::kResidual:
+                FLUX_LAUNCH_SPLIT(GemmEpilogue::kResidual);
+                break;
+            case GemmEpilogue::kSwiglu:
+                FLUX_LAUNCH_SPLIT(GemmEpilogue::kSwiglu);
+                break;
+            case GemmEpilogue::kQkvRope:
+                FLUX_LAUNCH_SPLIT(GemmEpilogue::kQkvRope);
+                break;
+        }
+#undef FLUX_LAUNCH_SPLIT
+        return hipGetLastError();
+    }
     const dim3 block(kGemmThreads);
     if ((epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) && args.n % kBN != 0 &&
         args.k % 32 == 0) {

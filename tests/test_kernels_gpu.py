@@ -243,11 +243,12 @@ def test_lm_head_argmax(gpu_device, vocab):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 16), (70, 576, 48), (64, 192, 32), (130, 960, 576), (257, 576, 1536),
-                                   (1024, 3072, 576)])
+                                   (512, 576, 1536), (600, 1024, 576), (1000, 576, 1536), (1024, 3072, 576)])
 def test_mfma_linear(gpu_device, m, n, k):
-    # Widths that are not a multiple of 128 take the 64 x 64 tile kernel when k % 32 == 0
-    # (192, 960 and 576 with k = 32, 576, 1536), else the 128-column kernel. Grids under 256 blocks
-    # take the four-buffer ring variants (all but the 1024-row case).
+    # Up to 512 rows: the split-K kernel (one 32 x 64 tile per block). Above that, widths that
+    # are not a multiple of 128 take the 64 x 64 tile kernel when k % 32 == 0, else the
+    # 128-column kernel; grids under 256 blocks take their four-buffer ring variants
+    # (600 and 1000 rows).
     a = _randn(m, k, seed=61).to(gpu_device)
     w = _randn(n, k, seed=62, std=0.05).to(gpu_device)
     r = _randn(m, n, seed=63).to(gpu_device)
