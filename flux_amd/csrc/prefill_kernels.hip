@@ -765,7 +765,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs
 // ---------------------------------------------------------------------------
 // Causal GQA prefill attention on v_mfma_f32_32x32x2f32.
 //
-// Block = (128-query tile, query head, chunk of at most kChunkTiles 64-key tiles);
+// Block = (128-query tile, query head, chunk of at most attn_chunk_tiles(seq) 64-key tiles);
 // 4 waves x 32 queries.  Per 64-key tile a wave computes S^T = K Q^T as two 32x32
 // tiles (32 MFMAs each: instruction s pairs dims s and s + 32), then
 // O^T += V^T P^T (16 MFMAs per 32 keys and 32-dim half): the S^T accumulator of a
@@ -780,7 +780,9 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs
 // variable, so reads of one never wait on copies into another.  Three blocks fit a
 // CU (49 KB of LDS, at most 168 VGPRs), i.e. three waves per SIMD.
 //
-// A query tile's keys are split into chunks of kChunkTiles tiles; a tile with one
+// A query tile's keys are split into chunks of attn_chunk_tiles(seq) tiles: about one
+// CU's even share of the causal work, so short prompts still spread over the device,
+// and at most kMaxChunkTiles (1536 keys) for long ones.  A tile with one
 // chunk writes its rows directly, longer ones write (o, m, l) partials that
 // prefill_attention_merge_kernel combines
 // (csrc/streaming_prefill_gqa/streaming_prefill_gqa_cuda.cu splits the keys into
@@ -789,9 +791,9 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs
 constexpr int kQTile = 128;
 constexpr int kKTile = 64;
 constexpr int kAttnThreads = 256;
-constexpr int kChunkTiles = 24;
+constexpr int kMaxChunkTiles = 24;
 constexpr int kPartialRow = kHeadDim + 4;  // o[64], m, l, 2 words of padding (16-byte rows)
-constexpr int kMergeMaxChunks = 16;        // kMaxCapacity / (kChunkTiles * kKTile)
+constexpr int kMergeMaxChunks = 16;        // >= the chunks of any query tile up to kMaxCapacity
 constexpr int kKVTileFloats = kKTile * kHeadDim;
 
 __host__ __device__ __forceinline__ int64_t attn_q_tiles(int64_t seq) { return (seq + kQTile - 1) / kQTile; }
@@ -799,14 +801,24 @@ __host__ __device__ __forceinline__ int64_t attn_key_tiles(int64_t seq, int64_t 
     const int64_t last = (qt + 1) * kQTile - 1 < seq - 1 ? (qt + 1) * kQTile - 1 : seq - 1;
     return last / kKTile + 1;
 }
-__host__ __device__ __forceinline__ int64_t attn_chunks(int64_t seq, int64_t qt) {
-    return (attn_key_tiles(seq, qt) + kChunkTiles - 1) / kChunkTiles;
+// Key tiles per chunk: the 9 heads' causal tile steps (query tile qt walks 2 (qt + 1)
+// key tiles) divided over 256 CUs, rounded up to an even count in [2, kMaxChunkTiles].
+// Even, because each query tile adds two key tiles.
+__host__ __device__ __forceinline__ int64_t attn_chunk_tiles(int64_t seq) {
+    const int64_t q = attn_q_tiles(seq);
+    const int64_t share = (kQHeads * q * (q + 1) + 255) / 256;
+    const int64_t even = (share + 1) / 2 * 2;
+    return even < 2 ? 2 : (even > kMaxChunkTiles ? kMaxChunkTiles : even);
 }
-// Query tiles below kLongTile have a single chunk.
-constexpr int64_t kLongTile = kChunkTiles * kKTile / kQTile;  // 12
+__host__ __device__ __forceinline__ int64_t attn_chunks(int64_t seq, int64_t qt) {
+    const int64_t ct = attn_chunk_tiles(seq);
+    return (attn_key_tiles(seq, qt) + ct - 1) / ct;
+}
+// Query tiles below attn_long_tile(seq) have a single chunk.
+__host__ __device__ __forceinline__ int64_t attn_long_tile(int64_t seq) { return attn_chunk_tiles(seq) * kKTile / kQTile; }
 __host__ __device__ __forceinline__ int64_t attn_max_chunks(int64_t seq) { return attn_chunks(seq, attn_q_tiles(seq) - 1); }
 __host__ __device__ __forceinline__ int64_t attn_partial_slot(int64_t seq, int64_t qt, int h, int64_t c) {
-    return ((qt - kLongTile) * kQHeads + h) * attn_max_chunks(seq) + c;
+    return ((qt - attn_long_tile(seq)) * kQHeads + h) * attn_max_chunks(seq) + c;
 }
 // Items of one head, longest first: every chunk of the last query tile, then the
 // full chunks of the others (chunk-major), then their partial last chunks by
@@ -819,6 +831,7 @@ __host__ __device__ __forceinline__ int64_t attn_items(int64_t seq) {
 }
 __device__ __forceinline__ void attn_item(int64_t seq, int64_t i, int64_t& qt, int64_t& chunk) {
     const int64_t q_tiles = attn_q_tiles(seq);
+    const int64_t ct = attn_chunk_tiles(seq);
     const int64_t last_chunks = attn_chunks(seq, q_tiles - 1);
     if (i < last_chunks) {
         qt = q_tiles - 1;
@@ -826,9 +839,9 @@ __device__ __forceinline__ void attn_item(int64_t seq, int64_t i, int64_t& qt, i
         return;
     }
     i -= last_chunks;
-    // Full chunk c of inner tile qt needs 2 (qt + 1) >= kChunkTiles (c + 1).
+    // Full chunk c of inner tile qt needs 2 (qt + 1) >= ct (c + 1).
     for (int64_t c = 0;; ++c) {
-        const int64_t first = kChunkTiles / 2 * (c + 1) - 1;
+        const int64_t first = ct / 2 * (c + 1) - 1;
         const int64_t count = q_tiles - 1 - first > 0 ? q_tiles - 1 - first : 0;
         if (count == 0) break;
         if (i < count) {
@@ -838,13 +851,13 @@ __device__ __forceinline__ void attn_item(int64_t seq, int64_t i, int64_t& qt, i
         }
         i -= count;
     }
-    // Partial chunks: length 2 (qt + 1) mod kChunkTiles = len, longest first.
-    for (int64_t len = kChunkTiles - 2; len >= 2; len -= 2) {
+    // Partial chunks: length 2 (qt + 1) mod ct = len, longest first.
+    for (int64_t len = ct - 2; len >= 2; len -= 2) {
         const int64_t r0 = len / 2 - 1;
-        const int64_t count = q_tiles - 2 - r0 >= 0 ? (q_tiles - 2 - r0) / (kChunkTiles / 2) + 1 : 0;
+        const int64_t count = q_tiles - 2 - r0 >= 0 ? (q_tiles - 2 - r0) / (ct / 2) + 1 : 0;
         if (i < count) {
-            qt = r0 + (kChunkTiles / 2) * i;
-            chunk = 2 * (qt + 1) / kChunkTiles;
+            qt = r0 + (ct / 2) * i;
+            chunk = 2 * (qt + 1) / ct;
             return;
         }
         i -= count;
@@ -912,8 +925,9 @@ prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ 
     const float* kg = key_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
     const float* vg = value_cache + static_cast<int64_t>(g) * capacity * kHeadDim;
     const int64_t k_tiles = attn_key_tiles(seq, qt);
-    const int64_t kt_begin = chunk * kChunkTiles;
-    const int64_t kt_end = kt_begin + kChunkTiles < k_tiles ? kt_begin + kChunkTiles : k_tiles;
+    const int64_t chunk_tiles = attn_chunk_tiles(seq);
+    const int64_t kt_begin = chunk * chunk_tiles;
+    const int64_t kt_end = kt_begin + chunk_tiles < k_tiles ? kt_begin + chunk_tiles : k_tiles;
 
     // Copies of key tile kt: K slot s (16 bytes) of the padded tile holds piece s % 17
     // of row s / 17 (piece 16 is padding and repeats piece 0); V slot s holds piece
@@ -1099,14 +1113,14 @@ prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ 
 }
 
 // Combines the chunk partials of query tiles with more than one chunk.  Block
-// ((qt - kLongTile) * 9 + h) * 8 + row group; thread t -> row 16 * group + t / 16,
+// ((qt - attn_long_tile(seq)) * 9 + h) * 8 + row group; thread t -> row 16 * group + t / 16,
 // dims 4 (t % 16) .. + 3.  All chunk loads of a thread are issued before the combine.
 __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(const float* __restrict__ workspace,
                                                                                int64_t seq,
                                                                                float* __restrict__ out_rows) {
     constexpr int kRowsPerBlock = kAttnThreads / 16;
     const int64_t tile_head = blockIdx.x / (kQTile / kRowsPerBlock);
-    const int64_t qt = kLongTile + tile_head / kQHeads;
+    const int64_t qt = attn_long_tile(seq) + tile_head / kQHeads;
     const int h = static_cast<int>(tile_head % kQHeads);
     const int row = static_cast<int>(blockIdx.x % (kQTile / kRowsPerBlock)) * kRowsPerBlock +
                     static_cast<int>(threadIdx.x >> 4);
@@ -1258,7 +1272,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
 }
 
 size_t prefill_attention_workspace_floats(int64_t seq) {
-    const int64_t long_tiles = attn_q_tiles(seq) - kLongTile;
+    const int64_t long_tiles = attn_q_tiles(seq) - attn_long_tile(seq);
     if (long_tiles <= 0 || attn_max_chunks(seq) <= 1) return 0;
     return static_cast<size_t>(long_tiles * kQHeads * attn_max_chunks(seq) * kQTile * kPartialRow);
 }
@@ -1274,7 +1288,7 @@ hipError_t launch_prefill_attention(const float* q, const float* key_cache, cons
                        key_cache, value_cache, seq, capacity, scale, workspace, out_rows);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    const int64_t long_tiles = attn_q_tiles(seq) - kLongTile;
+    const int64_t long_tiles = attn_q_tiles(seq) - attn_long_tile(seq);
     if (long_tiles > 0 && attn_max_chunks(seq) > 1) {
         hipLaunchKernelGGL(prefill_attention_merge_kernel,
                            dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / (kAttnThreads / 16)))),

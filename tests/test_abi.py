@@ -83,12 +83,15 @@ def test_shape_constraints_are_rejected():
     assert lib.flux_gqa_decode_workspace_bytes(16385, ctypes.byref(size)) == _native.FLUX_ERROR_INVALID_VALUE
     assert lib.flux_gqa_decode_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 85 * 3 * 3 * 66 * 4
-    # Keys are split into 1536-key chunks: up to 1536 tokens no 128-query tile sees two.
-    assert lib.flux_prefill_attention_workspace_bytes(1536, ctypes.byref(size)) == _native.FLUX_OK
+    # Keys are split into chunks of 2 to 24 64-key tiles (longer for longer prompts): a single
+    # 128-query tile never needs partials.
+    assert lib.flux_prefill_attention_workspace_bytes(128, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 0
+    # 2048 tokens: 10-tile chunks; the 11 query tiles past the first 5 x 9 heads x 4 chunks
+    # x 128 rows x (64 + m + l + 2 pad) floats
     assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
-    # 4 query tiles past the first 12 x 9 heads x 2 chunks x 128 rows x (64 + m + l + 2 pad) floats
-    assert size.value == 4 * 9 * 2 * 128 * 68 * 4
+    assert size.value == 11 * 9 * 4 * 128 * 68 * 4
+    # 8192 tokens: 24-tile (1536-key) chunks, 52 query tiles past the first 12, 6 chunks
     assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 52 * 9 * 6 * 128 * 68 * 4
     dummy = ctypes.c_void_p(16)

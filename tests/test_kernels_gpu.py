@@ -313,8 +313,10 @@ def _attention_workspace(seq, device):
 @pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024),
                                           (1537, 1600), (2049, 2100), (3201, 3300), (4160, 4160)])
 def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
-    # From 1537 tokens on, query tiles see more than one 1536-key chunk: they take the
-    # split-key path and its merge (3201: three chunks and a one-query last tile).
+    # Keys are split into chunks of 2 (up to 512 tokens) to 24 (from 3072 tokens on) 64-key
+    # tiles; from 129 tokens on some query tiles see several chunks and take the split-key
+    # path and its merge (1024: 4-tile chunks, 3201: 24-tile chunks, three of them, and a
+    # one-query last tile).
     q = _randn(9, seq, D, seed=91).to(gpu_device)
     kc = _randn(3, capacity, D, seed=92).to(gpu_device)
     vc = _randn(3, capacity, D, seed=93).to(gpu_device)

@@ -195,7 +195,7 @@ def test_end_to_end_8192_plus_512_is_deterministic(smol_model):
 @pytest.mark.parametrize("length", [1537, 3001])
 def test_odd_length_prefill_matches_oracle(small_model, length):
     """Prompt lengths that end inside a 128-query attention tile and split the keys of the
-    later tiles into 1536-key chunks (3001: three chunks), through the whole native
+    later tiles into chunks (1537: 6-tile chunks, 3001: 22-tile chunks), through the whole native
     prefill, against the CPU oracle: last-row logits, greedy token, K/V cache rows."""
     g = torch.Generator().manual_seed(length)
     prompt = torch.randint(0, 128, (1, length), generator=g)
