@@ -497,14 +497,15 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
     }
 }
 
-// Few rows (short prompts): one block per 32 x 64 output tile, its kSplitWaves waves
-// splitting K into contiguous ranges.  A wave streams its range 16 K values at a time
-// (32 A rows and the tile's 64 B rows, 64 bytes each, laid out and swizzled as in
-// gemm_kernel) through a private ring of kSplitStages LDS buffers; while a stage's MFMAs run,
-// the next stage's operands are already in registers and the kSplitStages - 2 after it are
-// being copied.  No wave waits for another until the partial tiles meet in LDS.
-// They are summed in wave order (the result does not depend on timing), and wave w
-// then finishes accumulator registers 4w .. 4w + 3 through the shared epilogue.
+// Grids smaller than the device (short and mid-length prompts): one block per
+// (32 * RT) x 64 output tile, RT = 1, 2 or 4.  Its kSplitWaves waves are RT row tiles
+// of 32 times kSplitWaves / RT contiguous K ranges.  A wave streams its 32 A rows and the
+// tile's 64 B rows over its K range, 16 K values (64 bytes per row) at a time, laid out
+// and swizzled as in gemm_kernel, through a private ring of kSplitStages LDS buffers;
+// while a stage's MFMAs run, the next stage's operands are already in registers and the
+// kSplitStages - 2 after it are being copied.  No wave waits for another until the
+// partial tiles of one row tile meet in LDS (RT < 4).  They are summed in K order (the
+// result does not depend on timing), and the row tile's waves share its epilogue.
 constexpr int kSplitWaves = 4;
 constexpr int kSplitStages = 5;
 constexpr int kSplitRows = 96;  // 32 A rows + 64 B rows per stage
@@ -518,25 +519,29 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// kStages = K / (kSplitWaves * 16), fixed at compile time so the stage loop is straight-line
-// code and every wait names exactly the copies it needs.
-template <GemmEpilogue E, int kStages>
+// kStages = K / (kSplitWaves / RT * 16), fixed at compile time so the stage loop is
+// straight-line code and every wait names exactly the copies it needs.
+template <GemmEpilogue E, int kStages, int RT>
 __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs args) {
     static_assert(kSplitStages == 5, "the buffers below are spelled out");
+    static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per block");
+    constexpr int kParts = kSplitWaves / RT;  // K ranges per row tile
     // One variable per ring slot: a read of one slot then never waits for copies into another.
     __shared__ __align__(16) float r0[kSplitWaves][kSplitRows * kBK];
     __shared__ __align__(16) float r1[kSplitWaves][kSplitRows * kBK];
     __shared__ __align__(16) float r2[kSplitWaves][kSplitRows * kBK];
     __shared__ __align__(16) float r3[kSplitWaves][kSplitRows * kBK];
     __shared__ __align__(16) float r4[kSplitWaves][kSplitRows * kBK];
-    __shared__ float partial[kSplitWaves][2][16][64];
+    __shared__ float partial[kParts > 1 ? kSplitWaves : 1][2][16][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32;
+    const int row_tile = wave % RT;
+    const int part = wave / RT;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32 * RT + 32 * row_tile;
     const int n0 = blockIdx.x * 64;
     const int K = args.k;
-    constexpr int kSpan = kStages * kBK;  // this wave's K values start at wave * kSpan
+    constexpr int kSpan = kStages * kBK;  // this wave's K values start at part * kSpan
 
     const float* src[kSplitCopies];
 #pragma unroll
@@ -550,7 +555,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         } else {
             base = args.b + static_cast<int64_t>(b_row<E>(n0 + row - 32, args.n)) * K;
         }
-        src[i] = base + wave * kSpan + 4 * piece;
+        src[i] = base + part * kSpan + 4 * piece;
     }
     auto slot = [&](auto bi) -> float* {
         constexpr int b = decltype(bi)::value % kSplitStages;
@@ -616,24 +621,29 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         cur = nxt;
     });
     wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
+    if constexpr (kParts == 1) {
+        const f32x16(&whole)[1][2] = reinterpret_cast<const f32x16(&)[1][2]>(acc);
+        gemm_epilogue<E, 1>(args, whole, m0, n0, lane);
+    } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        partial[wave][0][r][lane] = acc[0][r];
-        partial[wave][1][r][lane] = acc[1][r];
-    }
-    __syncthreads();
-    const int j = lane & 31;
-#pragma unroll
-    for (int u = 0; u < 16 / kSplitWaves; ++u) {
-        const int r = (16 / kSplitWaves) * wave + u;
-        float lo = partial[0][0][r][lane], hi = partial[0][1][r][lane];
-#pragma unroll
-        for (int w = 1; w < kSplitWaves; ++w) {
-            lo += partial[w][0][r][lane];
-            hi += partial[w][1][r][lane];
+        for (int r = 0; r < 16; ++r) {
+            partial[wave][0][r][lane] = acc[0][r];
+            partial[wave][1][r][lane] = acc[1][r];
         }
-        const int64_t out_row = m0 + mfma32_row(lane, r);
-        if (out_row < args.m) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
+        __syncthreads();
+        const int j = lane & 31;
+#pragma unroll
+        for (int u = 0; u < 16 / kParts; ++u) {
+            const int r = (16 / kParts) * part + u;
+            float lo = partial[row_tile][0][r][lane], hi = partial[row_tile][1][r][lane];
+#pragma unroll
+            for (int p = 1; p < kParts; ++p) {
+                lo += partial[row_tile + RT * p][0][r][lane];
+                hi += partial[row_tile + RT * p][1][r][lane];
+            }
+            const int64_t out_row = m0 + mfma32_row(lane, r);
+            if (out_row < args.m) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
+        }
     }
 }
 
@@ -1186,17 +1196,28 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
-    const int split_stages = args.k % (kSplitWaves * kBK) == 0 ? args.k / (kSplitWaves * kBK) : 0;
-    if ((split_stages == 9 || split_stages == 24) && (args.n / 64) * ((args.m + 31) / 32) <= kSplitBlocks) {
-        // K = 576 (hidden) or 1536 (intermediate): one 32 x 64 tile per block.
-        const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 31) / 32));
+    // Smallest row tiling whose grid fits the device once; K = 576 (hidden) or 1536
+    // (intermediate).  Shapes the 64 x 64 tile kernel takes use one row tile only: with more,
+    // its 9 column tiles leave too many CUs idle (measured slower at 1024 to 2048 rows).
+    const bool narrow_shape = (epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) &&
+                              args.n % kBN != 0 && args.k % 32 == 0;
+    for (int rt = 1; rt <= (narrow_shape ? 1 : 4) && args.k % (kSplitWaves * kBK) == 0; rt *= 2) {
+        const int64_t tiles = (args.n / 64) * ((args.m + 32 * rt - 1) / (32 * rt));
+        const int hidden = args.k == kHidden, inter = args.k == kInter;
+        if (tiles > kSplitBlocks || !(hidden || inter)) continue;
+        const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
         const dim3 split_block(64 * kSplitWaves);
-#define FLUX_LAUNCH_SPLIT(E)                                                                                       \
-    do {                                                                                                           \
-        if (split_stages == 9)                                                                                     \
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, 9>), grid, split_block, 0, stream, args);      \
-        else                                                                                                       \
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, 24>), grid, split_block, 0, stream, args);     \
+#define FLUX_SPLIT_RT(E, ST, RT)                                                                        \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT>), grid, split_block, 0, stream, args)
+#define FLUX_LAUNCH_SPLIT(E)                                                                            \
+    do {                                                                                                \
+        if (rt == 1) {                                                                                  \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 1); else FLUX_SPLIT_RT(E, 24, 1);                           \
+        } else if (rt == 2) {                                                                           \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 2); else FLUX_SPLIT_RT(E, 24, 2);                           \
+        } else {                                                                                        \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 4); else FLUX_SPLIT_RT(E, 24, 4);                           \
+        }                                                                                               \
     } while (0)
         switch (epilogue) {
             case GemmEpilogue::kStore:
@@ -1213,6 +1234,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
                 break;
         }
 #undef FLUX_LAUNCH_SPLIT
+#undef FLUX_SPLIT_RT
         return hipGetLastError();
     }
     const dim3 block(kGemmThreads);
