@@ -98,9 +98,19 @@ struct GemmArgs {
     float* key_cache;       // [3, capacity, 64]
     float* value_cache;
     int64_t capacity;
+    // Optional RMSNorm folded into the GEMM (only gemm_split_kernel takes it): A holds the
+    // raw rows, each K value is scaled by norm_weight[k] and each output row by the inverse
+    // RMS of its A row.  launch_gemm rejects a norm it cannot fold; launch_norm_gemm folds it
+    // where it can and otherwise runs the RMSNorm kernel first.
+    const float* norm_weight;
+    float norm_eps;
 };
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream);
+// epilogue(rmsnorm(A) * W^T): args.a holds the raw rows; `scratch` ([M, K]) receives the
+// normalized rows when the norm cannot be folded into the GEMM.
+hipError_t launch_norm_gemm(const GemmArgs& args, const float* norm_weight, float eps, float* scratch,
+                            GemmEpilogue epilogue, hipStream_t stream);
 
 // Workspace (floats) of launch_prefill_attention for a prompt of `seq` tokens (0 when
 // every query tile fits in one key chunk).

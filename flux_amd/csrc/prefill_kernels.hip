@@ -521,7 +521,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // kStages = K / (kSplitWaves / RT * 16), fixed at compile time so the stage loop is
 // straight-line code and every wait names exactly the copies it needs.
-template <GemmEpilogue E, int kStages, int RT>
+template <GemmEpilogue E, int kStages, int RT, bool kNorm>
 __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs args) {
     static_assert(kSplitStages == 5, "the buffers below are spelled out");
     static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per block");
@@ -533,6 +533,8 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     __shared__ __align__(16) float r3[kSplitWaves][kSplitRows * kBK];
     __shared__ __align__(16) float r4[kSplitWaves][kSplitRows * kBK];
     __shared__ float partial[kParts > 1 ? kSplitWaves : 1][2][16][64];
+    __shared__ __align__(16) float norm_g[kNorm ? kHidden : 4];  // folded RMSNorm: weights of the K values
+    __shared__ float norm_ss[kNorm ? kSplitWaves : 1][32];       // folded RMSNorm: sums of squares per row
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -542,6 +544,19 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     const int n0 = blockIdx.x * 64;
     const int K = args.k;
     constexpr int kSpan = kStages * kBK;  // this wave's K values start at part * kSpan
+    static_assert(!kNorm || kStages * kBK * kParts == kHidden, "the folded norm spans the hidden width");
+    // Folded RMSNorm: the norm weights are requested before the first copies and stored to LDS
+    // after them, so their latency overlaps the copies'.
+    constexpr int kNormLoads = (kHidden + 64 * kSplitWaves - 1) / (64 * kSplitWaves);
+    float norm_load[kNormLoads];
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int i = 0; i < kNormLoads; ++i) {
+            const int k = threadIdx.x + 64 * kSplitWaves * i;
+            norm_load[i] = k < kHidden ? args.norm_weight[k] : 0.0f;
+        }
+    }
+    float ss = 0.0f;
 
     const float* src[kSplitCopies];
 #pragma unroll
@@ -585,21 +600,50 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     struct Operands {
         f32x4 a[2];
         f32x4 b[2][2];
+        f32x4 g[2];  // folded RMSNorm: the weights of the a values
     };
     auto read = [&](auto st, Operands& o) {
         const float* t = slot(st);
         o.a[0] = *reinterpret_cast<const f32x4*>(t + a_off0);
         o.a[1] = *reinterpret_cast<const f32x4*>(t + a_off1);
+        if constexpr (kNorm) {
+            // This lane's K values: pieces 2h and 2h + 1 of the stage.
+            const float* g = norm_g + part * kSpan + decltype(st)::value * kBK + 8 * h;
+            o.g[0] = *reinterpret_cast<const f32x4*>(g);
+            o.g[1] = *reinterpret_cast<const f32x4*>(g + 4);
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 2; ++q) o.b[j][q] = *reinterpret_cast<const f32x4*>(t + b_off[j][q]);
     };
+    // Folded RMSNorm: accumulate the squares of a stage's raw A values, then scale them by the
+    // norm weights of their K indices.
+    auto fold_norm = [&](Operands& o) {
+        if constexpr (kNorm) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ss = fmaf(o.a[q][e], o.a[q][e], ss);
+                    o.a[q][e] *= o.g[q][e];
+                }
+        }
+    };
     constexpr int kAhead = kSplitStages - 1;  // stages issued before the loop
     static_for<0, (kStages < kAhead ? kStages : kAhead)>([&](auto st) { issue(st); });
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int i = 0; i < kNormLoads; ++i) {
+            const int k = threadIdx.x + 64 * kSplitWaves * i;
+            if (k < kHidden) norm_g[k] = norm_load[i];
+        }
+        lds_barrier();  // waits for LDS traffic only, not for the copies in flight
+    }
     Operands cur, nxt;
     wait_vmcnt<((kStages < kAhead ? kStages : kAhead) - 1) * kSplitCopies>();
     read(std::integral_constant<int, 0>{}, cur);
+    fold_norm(cur);
     static_for<0, kStages>([&](auto st) {
         constexpr int s = decltype(st)::value;
         // Slot (s + kAhead) % kSplitStages last held stage s - 1, whose operands were read in
@@ -618,10 +662,33 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[kk >> 2][kk & 3], cur.b[j][kk >> 2][kk & 3], acc[j],
                                                               0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
+        // The folded norm scales the next stage's operands once this stage's MFMAs have issued:
+        // its reads have landed by then, and no MFMA in flight reads those registers.
+        if constexpr (s + 1 < kStages) fold_norm(nxt);
         cur = nxt;
     });
     wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
+    if constexpr (kNorm) {
+        ss += __shfl_xor(ss, 32, 64);  // the two K halves of the lane's row
+        if (lane < 32) norm_ss[wave][lane] = ss;
+    }
+    // Inverse RMS of output row `row` (0..31) of this wave's row tile, summed over the K parts
+    // in order; read after the block barrier below (kParts > 1) or this wave's own writes.
+    auto row_scale = [&](int row) {
+        float total = norm_ss[kNorm ? row_tile : 0][row];
+#pragma unroll
+        for (int p = 1; p < kParts; ++p) total += norm_ss[kNorm ? row_tile + RT * p : 0][row];
+        return rms_inverse(total, kHidden, args.norm_eps);
+    };
     if constexpr (kParts == 1) {
+        if constexpr (kNorm) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float inv = row_scale(mfma32_row(lane, r));
+                acc[0][r] *= inv;
+                acc[1][r] *= inv;
+            }
+        }
         const f32x16(&whole)[1][2] = reinterpret_cast<const f32x16(&)[1][2]>(acc);
         gemm_epilogue<E, 1>(args, whole, m0, n0, lane);
     } else {
@@ -640,6 +707,11 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
             for (int p = 1; p < kParts; ++p) {
                 lo += partial[row_tile + RT * p][0][r][lane];
                 hi += partial[row_tile + RT * p][1][r][lane];
+            }
+            if constexpr (kNorm) {
+                const float inv = row_scale(mfma32_row(lane, r));
+                lo *= inv;
+                hi *= inv;
             }
             const int64_t out_row = m0 + mfma32_row(lane, r);
             if (out_row < args.m) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
@@ -1192,32 +1264,53 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 constexpr int64_t kRingBlocks = 256;
 constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
 
+// Row tiles per block of gemm_split_kernel for this GEMM, or 0 when it does not take it: the
+// smallest tiling whose grid fits the device once, for K = 576 (hidden) or 1536
+// (intermediate).  Shapes the 64 x 64 tile kernel takes use one row tile only: with more,
+// their 9 column tiles leave too many CUs idle (measured slower at 1024 to 2048 rows).
+static int split_row_tiles(const GemmArgs& args, GemmEpilogue epilogue) {
+    if (args.k != kHidden && args.k != kInter) return 0;
+    const bool narrow_shape = (epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) &&
+                              args.n % kBN != 0 && args.k % 32 == 0;
+    for (int rt = 1; rt <= (narrow_shape ? 1 : 4); rt *= 2)
+        if ((args.n / 64) * ((args.m + 32 * rt - 1) / (32 * rt)) <= kSplitBlocks) return rt;
+    return 0;
+}
+
+// gemm_split_kernel folds an RMSNorm of the A rows into the QKV and gate/up GEMMs (K = hidden).
+static bool split_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) {
+    return args.k == kHidden && (epilogue == GemmEpilogue::kQkvRope || epilogue == GemmEpilogue::kSwiglu) &&
+           split_row_tiles(args, epilogue) != 0;
+}
+
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
-    // Smallest row tiling whose grid fits the device once; K = 576 (hidden) or 1536
-    // (intermediate).  Shapes the 64 x 64 tile kernel takes use one row tile only: with more,
-    // its 9 column tiles leave too many CUs idle (measured slower at 1024 to 2048 rows).
-    const bool narrow_shape = (epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) &&
-                              args.n % kBN != 0 && args.k % 32 == 0;
-    for (int rt = 1; rt <= (narrow_shape ? 1 : 4) && args.k % (kSplitWaves * kBK) == 0; rt *= 2) {
-        const int64_t tiles = (args.n / 64) * ((args.m + 32 * rt - 1) / (32 * rt));
-        const int hidden = args.k == kHidden, inter = args.k == kInter;
-        if (tiles > kSplitBlocks || !(hidden || inter)) continue;
+    const int rt = split_row_tiles(args, epilogue);
+    const bool norm = args.norm_weight != nullptr;
+    if (norm && !split_folds_norm(args, epilogue)) return hipErrorInvalidValue;
+    if (rt != 0) {
+        const bool hidden = args.k == kHidden;
         const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
         const dim3 split_block(64 * kSplitWaves);
-#define FLUX_SPLIT_RT(E, ST, RT)                                                                        \
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT>), grid, split_block, 0, stream, args)
+#define FLUX_SPLIT_RT(E, ST, RT, NORM)                                                                  \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT, NORM>), grid, split_block, 0, stream, args)
 #define FLUX_LAUNCH_SPLIT(E)                                                                            \
     do {                                                                                                \
         if (rt == 1) {                                                                                  \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 1); else FLUX_SPLIT_RT(E, 24, 1);                           \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 1, false); else FLUX_SPLIT_RT(E, 24, 1, false);             \
         } else if (rt == 2) {                                                                           \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 2); else FLUX_SPLIT_RT(E, 24, 2);                           \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 2, false); else FLUX_SPLIT_RT(E, 24, 2, false);             \
         } else {                                                                                        \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 4); else FLUX_SPLIT_RT(E, 24, 4);                           \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 4, false); else FLUX_SPLIT_RT(E, 24, 4, false);             \
         }                                                                                               \
+    } while (0)
+#define FLUX_LAUNCH_SPLIT_NORM(E)                                                                       \
+    do {                                                                                                \
+        if (rt == 1) FLUX_SPLIT_RT(E, 9, 1, true);                                                      \
+        else if (rt == 2) FLUX_SPLIT_RT(E, 9, 2, true);                                                 \
+        else FLUX_SPLIT_RT(E, 9, 4, true);                                                              \
     } while (0)
         switch (epilogue) {
             case GemmEpilogue::kStore:
@@ -1227,12 +1320,15 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
                 FLUX_LAUNCH_SPLIT(GemmEpilogue::kResidual);
                 break;
             case GemmEpilogue::kSwiglu:
-                FLUX_LAUNCH_SPLIT(GemmEpilogue::kSwiglu);
+                if (norm) FLUX_LAUNCH_SPLIT_NORM(GemmEpilogue::kSwiglu);
+                else FLUX_LAUNCH_SPLIT(GemmEpilogue::kSwiglu);
                 break;
             case GemmEpilogue::kQkvRope:
-                FLUX_LAUNCH_SPLIT(GemmEpilogue::kQkvRope);
+                if (norm) FLUX_LAUNCH_SPLIT_NORM(GemmEpilogue::kQkvRope);
+                else FLUX_LAUNCH_SPLIT(GemmEpilogue::kQkvRope);
                 break;
         }
+#undef FLUX_LAUNCH_SPLIT_NORM
 #undef FLUX_LAUNCH_SPLIT
 #undef FLUX_SPLIT_RT
         return hipGetLastError();
@@ -1291,6 +1387,22 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     }
 #undef FLUX_LAUNCH_GEMM
     return hipGetLastError();
+}
+
+hipError_t launch_norm_gemm(const GemmArgs& args, const float* norm_weight, float eps, float* scratch,
+                            GemmEpilogue epilogue, hipStream_t stream) {
+    if (split_folds_norm(args, epilogue)) {
+        GemmArgs folded = args;
+        folded.norm_weight = norm_weight;
+        folded.norm_eps = eps;
+        return launch_gemm(folded, epilogue, stream);
+    }
+    const hipError_t e = launch_rmsnorm_rows(args.a, norm_weight, scratch, args.m, args.k, eps, stream);
+    if (e != hipSuccess) return e;
+    GemmArgs plain = args;
+    plain.a = scratch;
+    plain.norm_weight = nullptr;
+    return launch_gemm(plain, epilogue, stream);
 }
 
 size_t prefill_attention_workspace_floats(int64_t seq) {

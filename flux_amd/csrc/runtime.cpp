@@ -542,10 +542,8 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
     for (int layer = 0; layer < kLayers; ++layer) {
         float* keys = db.key_cache + layer * layer_elems;
         float* values = db.value_cache + layer * layer_elems;
-        check_hip(launch_rmsnorm_rows(hidden_a_, weights_.input_norm[layer], norm_, seq_, kHidden, eps_[layer], stream),
-                  "launching input RMSNorm");
         GemmArgs qkv{};
-        qkv.a = norm_;
+        qkv.a = hidden_a_;
         qkv.b = weights_.packed_qkv[layer];
         qkv.m = seq_;
         qkv.n = kQKV;
@@ -556,7 +554,8 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         qkv.key_cache = keys;
         qkv.value_cache = values;
         qkv.capacity = capacity_;
-        check_hip(launch_gemm(qkv, GemmEpilogue::kQkvRope, stream), "launching QKV GEMM");
+        check_hip(launch_norm_gemm(qkv, weights_.input_norm[layer], eps_[layer], norm_, GemmEpilogue::kQkvRope, stream),
+                  "launching input RMSNorm + QKV GEMM");
         check_hip(launch_prefill_attention(query_, keys, values, seq_, capacity_, scales_[layer], attn_workspace_,
                                            attn_rows_, stream),
                   "launching prefill attention");
@@ -569,16 +568,15 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         o.n = kHidden;
         o.k = kHidden;
         check_hip(launch_gemm(o, GemmEpilogue::kResidual, stream), "launching o_proj GEMM");
-        check_hip(launch_rmsnorm_rows(hidden_b_, weights_.post_norm[layer], norm_, seq_, kHidden, eps_[layer], stream),
-                  "launching post-attention RMSNorm");
         GemmArgs gu{};
-        gu.a = norm_;
+        gu.a = hidden_b_;
         gu.b = weights_.gate_up[layer];
         gu.c = swiglu_;
         gu.m = seq_;
         gu.n = kGateUp;
         gu.k = kHidden;
-        check_hip(launch_gemm(gu, GemmEpilogue::kSwiglu, stream), "launching gate/up GEMM");
+        check_hip(launch_norm_gemm(gu, weights_.post_norm[layer], eps_[layer], norm_, GemmEpilogue::kSwiglu, stream),
+                  "launching post-attention RMSNorm + gate/up GEMM");
         GemmArgs dn{};
         dn.a = swiglu_;
         dn.b = weights_.down[layer];
