@@ -192,12 +192,13 @@ def test_end_to_end_8192_plus_512_is_deterministic(smol_model):
     assert runtime.device_error() == 0
 
 
-@pytest.mark.parametrize("length", [333, 1537, 3001])
+@pytest.mark.parametrize("length", [1, 45, 333, 1537, 3001])
 def test_odd_length_prefill_matches_oracle(small_model, length):
     """Prompt lengths that end inside a 128-query attention tile and split the keys of the
     later tiles into chunks (333: 2-tile, 1537: 6-tile, 3001: 22-tile chunks), through the whole
     native prefill, against the CPU oracle: last-row logits, greedy token, K/V cache rows.
-    333 and 1537 rows also take the GEMMs that fold the RMSNorm (QKV at both, gate/up at 333)."""
+    1 to 1537 rows also take the GEMMs that fold the RMSNorm (QKV at all four, gate/up up to 333;
+    1 and 45 rows end inside the first 32-row tile)."""
     g = torch.Generator().manual_seed(length)
     prompt = torch.randint(0, 128, (1, length), generator=g)
     runtime = NativeSmolLM2Prefill.capture(small_model, prompt.cuda(), max_decode_steps=1)
@@ -210,7 +211,7 @@ def test_odd_length_prefill_matches_oracle(small_model, length):
     torch.testing.assert_close(logits, expected, atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
     if top2_margin(expected) > 1e-3:
         assert int(runtime.current_token.item()) == int(torch.argmax(expected))
-    positions = torch.tensor(sorted({p for p in (0, 1535, 1536, length - 2, length - 1) if p < length}))
+    positions = torch.tensor(sorted({p for p in (0, 1535, 1536, length - 2, length - 1) if 0 <= p < length}))
     for layer in (0, 29):
         k = runtime.key_cache[layer, 0][:, positions].float().cpu()
         v = runtime.value_cache[layer, 0][:, positions].float().cpu()
