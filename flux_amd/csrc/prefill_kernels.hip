@@ -863,7 +863,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs
 // CU (49 KB of LDS, at most 168 VGPRs), i.e. three waves per SIMD.
 //
 // A query tile's keys are split into chunks of attn_chunk_tiles(seq) tiles: about one
-// CU's even share of the causal work, so short prompts still spread over the device,
+// block slot's even share of the causal work, so short prompts still spread over the device,
 // and at most kMaxChunkTiles (1536 keys) for long ones.  A tile with one
 // chunk writes its rows directly, longer ones write (o, m, l) partials that
 // prefill_attention_merge_kernel combines
@@ -884,11 +884,13 @@ __host__ __device__ __forceinline__ int64_t attn_key_tiles(int64_t seq, int64_t 
     return last / kKTile + 1;
 }
 // Key tiles per chunk: the 9 heads' causal tile steps (query tile qt walks 2 (qt + 1)
-// key tiles) divided over 256 CUs, rounded up to an even count in [2, kMaxChunkTiles].
-// Even, because each query tile adds two key tiles.
+// key tiles) divided over the device's 768 block slots (256 CUs x 3 resident blocks),
+// rounded up to an even count in [2, kMaxChunkTiles].  Even, because each query tile adds
+// two key tiles.  (Dividing over 256, 512, 1024 or 1536 instead measured slower at 2048 to
+// 4096 tokens.)
 __host__ __device__ __forceinline__ int64_t attn_chunk_tiles(int64_t seq) {
     const int64_t q = attn_q_tiles(seq);
-    const int64_t share = (kQHeads * q * (q + 1) + 255) / 256;
+    const int64_t share = (kQHeads * q * (q + 1) + 767) / 768;
     const int64_t even = (share + 1) / 2 * 2;
     return even < 2 ? 2 : (even > kMaxChunkTiles ? kMaxChunkTiles : even);
 }

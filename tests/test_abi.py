@@ -87,10 +87,10 @@ def test_shape_constraints_are_rejected():
     # 128-query tile never needs partials.
     assert lib.flux_prefill_attention_workspace_bytes(128, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 0
-    # 2048 tokens: 10-tile chunks; the 11 query tiles past the first 5 x 9 heads x 4 chunks
+    # 2048 tokens: 4-tile chunks; the 14 query tiles past the first 2 x 9 heads x 8 chunks
     # x 128 rows x (64 + m + l + 2 pad) floats
     assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
-    assert size.value == 11 * 9 * 4 * 128 * 68 * 4
+    assert size.value == 14 * 9 * 8 * 128 * 68 * 4
     # 8192 tokens: 24-tile (1536-key) chunks, 52 query tiles past the first 12, 6 chunks
     assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 52 * 9 * 6 * 128 * 68 * 4

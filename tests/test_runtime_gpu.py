@@ -195,7 +195,7 @@ def test_end_to_end_8192_plus_512_is_deterministic(smol_model):
 @pytest.mark.parametrize("length", [1, 45, 333, 1537, 3001])
 def test_odd_length_prefill_matches_oracle(small_model, length):
     """Prompt lengths that end inside a 128-query attention tile and split the keys of the
-    later tiles into chunks (333: 2-tile, 1537: 6-tile, 3001: 22-tile chunks), through the whole
+    later tiles into chunks (333: 2-tile, 1537: 4-tile, 3001: 8-tile chunks), through the whole
     native prefill, against the CPU oracle: last-row logits, greedy token, K/V cache rows.
     1 to 1537 rows also take the GEMMs that fold the RMSNorm (QKV at all four, gate/up up to 333;
     1 and 45 rows end inside the first 32-row tile)."""
