@@ -13,10 +13,15 @@
 //    epilogue consumes the accumulator layout directly: the two column tiles of a
 //    wave hold columns j and j+32 of the same rows, which is exactly the RoPE pair
 //    (a 64-column group = one head) and the gate/up pair (gate/up rows are
-//    interleaved 32+32 per group).
+//    interleaved 32+32 per group).  N = 576 outputs (o_proj, down) use 64x64 tiles.
+//    Grids smaller than the device (short prompts) use copy-ring variants, or, for
+//    K = 576 / 1536, a split-K kernel whose waves stream private LDS rings and which
+//    folds the preceding RMSNorm into the QKV and gate/up GEMMs.
 //  * Attention: one block per (128-query tile, query head, key chunk); 4 waves x 32
 //    queries.  S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x2f32, so the S^T
-//    accumulators are already the B operand of the PV product (no transpose).
+//    accumulators are already the B operand of the PV product (no transpose).  The
+//    chunk length follows the prompt length; chunk partials are merged by a second
+//    kernel.
 
 #include "flux_common.h"
 #include "flux_kernels.h"
