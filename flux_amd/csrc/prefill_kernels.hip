@@ -116,6 +116,18 @@ __device__ __forceinline__ void gemm_store_pair(const GemmArgs& args, int64_t ro
     }
 }
 
+// One output value of the plain or residual epilogue.
+template <GemmEpilogue E>
+__device__ __forceinline__ void gemm_store_one(const GemmArgs& args, int64_t row, int col, float v) {
+    static_assert(E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual, "plain epilogues only");
+    const int64_t i0 = row * args.n + col;
+    if constexpr (E == GemmEpilogue::kResidual) {
+        args.c[i0] = args.residual[i0] + v;
+    } else {
+        args.c[i0] = v;
+    }
+}
+
 template <GemmEpilogue E, int MI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const f32x16 (&acc)[MI][2], int64_t row0, int g0,
                                               int lane) {
@@ -513,8 +525,6 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
 // result does not depend on timing), and the row tile's waves share its epilogue.
 constexpr int kSplitWaves = 4;
 constexpr int kSplitStages = 5;
-constexpr int kSplitRows = 96;  // 32 A rows + 64 B rows per stage
-constexpr int kSplitCopies = kSplitRows / 16;
 
 template <int S, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -526,18 +536,26 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // kStages = K / (kSplitWaves / RT * 16), fixed at compile time so the stage loop is
 // straight-line code and every wait names exactly the copies it needs.
-template <GemmEpilogue E, int kStages, int RT, bool kNorm>
+template <GemmEpilogue E, int kStages, int RT, bool kNorm, int kCols>
 __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs args) {
     static_assert(kSplitStages == 5, "the buffers below are spelled out");
     static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per block");
+    // kCols = 64 (two 32-column MFMA tiles: the RoPE / SwiGLU pair layout) or 32 (plain and
+    // residual epilogues only: twice the blocks, half the MFMAs per wave).
+    static_assert(kCols == 64 || (kCols == 32 && !kNorm &&
+                                  (E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual)),
+                  "32-column tiles carry no column pairs");
+    constexpr int kTiles = kCols / 32;
+    constexpr int kRows = 32 + kCols;  // A rows + B rows per stage
+    constexpr int kCopies = kRows / 16;
     constexpr int kParts = kSplitWaves / RT;  // K ranges per row tile
     // One variable per ring slot: a read of one slot then never waits for copies into another.
-    __shared__ __align__(16) float r0[kSplitWaves][kSplitRows * kBK];
-    __shared__ __align__(16) float r1[kSplitWaves][kSplitRows * kBK];
-    __shared__ __align__(16) float r2[kSplitWaves][kSplitRows * kBK];
-    __shared__ __align__(16) float r3[kSplitWaves][kSplitRows * kBK];
-    __shared__ __align__(16) float r4[kSplitWaves][kSplitRows * kBK];
-    __shared__ float partial[kParts > 1 ? kSplitWaves : 1][2][16][64];
+    __shared__ __align__(16) float r0[kSplitWaves][kRows * kBK];
+    __shared__ __align__(16) float r1[kSplitWaves][kRows * kBK];
+    __shared__ __align__(16) float r2[kSplitWaves][kRows * kBK];
+    __shared__ __align__(16) float r3[kSplitWaves][kRows * kBK];
+    __shared__ __align__(16) float r4[kSplitWaves][kRows * kBK];
+    __shared__ float partial[kParts > 1 ? kSplitWaves : 1][kTiles][16][64];
     __shared__ __align__(16) float norm_g[kNorm ? kHidden : 4];  // folded RMSNorm: weights of the K values
     __shared__ float norm_ss[kNorm ? kSplitWaves : 1][32];       // folded RMSNorm: sums of squares per row
 
@@ -546,7 +564,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     const int row_tile = wave % RT;
     const int part = wave / RT;
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32 * RT + 32 * row_tile;
-    const int n0 = blockIdx.x * 64;
+    const int n0 = blockIdx.x * kCols;
     const int K = args.k;
     constexpr int kSpan = kStages * kBK;  // this wave's K values start at part * kSpan
     static_assert(!kNorm || kStages * kBK * kParts == kHidden, "the folded norm spans the hidden width");
@@ -563,9 +581,9 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     }
     float ss = 0.0f;
 
-    const float* src[kSplitCopies];
+    const float* src[kCopies];
 #pragma unroll
-    for (int i = 0; i < kSplitCopies; ++i) {
+    for (int i = 0; i < kCopies; ++i) {
         const int row = 16 * i + (lane >> 2);
         const int piece = (lane & 3) ^ ((row >> 2) & 3);
         const float* base;
@@ -588,23 +606,24 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     auto issue = [&](auto st) {
         float* dst = slot(st);
 #pragma unroll
-        for (int i = 0; i < kSplitCopies; ++i) lds_copy16(src[i] + decltype(st)::value * kBK, dst + i * 16 * kBK);
+        for (int i = 0; i < kCopies; ++i) lds_copy16(src[i] + decltype(st)::value * kBK, dst + i * 16 * kBK);
     };
 
     const int h = lane >> 5;
     const int ra = lane & 31;
     const int a_off0 = tile_offset(ra, 2 * h), a_off1 = tile_offset(ra, 2 * h + 1);
-    const int b_off[2][2] = {{tile_offset(32 + ra, 2 * h), tile_offset(32 + ra, 2 * h + 1)},
-                             {tile_offset(64 + ra, 2 * h), tile_offset(64 + ra, 2 * h + 1)}};
-    f32x16 acc[2];
+    int b_off[kTiles][2];
+    f32x16 acc[kTiles];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        acc[0][r] = 0.0f;
-        acc[1][r] = 0.0f;
+    for (int j = 0; j < kTiles; ++j) {
+        b_off[j][0] = tile_offset(32 + 32 * j + ra, 2 * h);
+        b_off[j][1] = tile_offset(32 + 32 * j + ra, 2 * h + 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
     }
     struct Operands {
         f32x4 a[2];
-        f32x4 b[2][2];
+        f32x4 b[kTiles][2];
         f32x4 g[2];  // folded RMSNorm: the weights of the a values
     };
     auto read = [&](auto st, Operands& o) {
@@ -618,7 +637,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
             o.g[1] = *reinterpret_cast<const f32x4*>(g + 4);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kTiles; ++j)
 #pragma unroll
             for (int q = 0; q < 2; ++q) o.b[j][q] = *reinterpret_cast<const f32x4*>(t + b_off[j][q]);
     };
@@ -646,7 +665,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         lds_barrier();  // waits for LDS traffic only, not for the copies in flight
     }
     Operands cur, nxt;
-    wait_vmcnt<((kStages < kAhead ? kStages : kAhead) - 1) * kSplitCopies>();
+    wait_vmcnt<((kStages < kAhead ? kStages : kAhead) - 1) * kCopies>();
     read(std::integral_constant<int, 0>{}, cur);
     fold_norm(cur);
     static_for<0, kStages>([&](auto st) {
@@ -655,7 +674,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         // step s - 2 and consumed in step s - 1.
         if constexpr (s + 1 < kStages) {
             constexpr int newest = s + kAhead - 1 < kStages ? s + kAhead - 1 : kStages - 1;
-            wait_vmcnt<(newest - s - 1) * kSplitCopies>();
+            wait_vmcnt<(newest - s - 1) * kCopies>();
             read(std::integral_constant<int, s + 1>{}, nxt);
         }
         if constexpr (s + kAhead < kStages) issue(std::integral_constant<int, s + kAhead>{});
@@ -663,7 +682,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < kTiles; ++j)
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[kk >> 2][kk & 3], cur.b[j][kk >> 2][kk & 3], acc[j],
                                                               0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -685,7 +704,13 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         for (int p = 1; p < kParts; ++p) total += norm_ss[kNorm ? row_tile + RT * p : 0][row];
         return rms_inverse(total, kHidden, args.norm_eps);
     };
-    if constexpr (kParts == 1) {
+    if constexpr (kParts == 1 && kCols == 32) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t out_row = m0 + mfma32_row(lane, r);
+            if (out_row < args.m) gemm_store_one<E>(args, out_row, n0 + (lane & 31), acc[0][r]);
+        }
+    } else if constexpr (kParts == 1) {
         if constexpr (kNorm) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -694,24 +719,23 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
                 acc[1][r] *= inv;
             }
         }
-        const f32x16(&whole)[1][2] = reinterpret_cast<const f32x16(&)[1][2]>(acc);
+        const f32x16(&whole)[1][2] = reinterpret_cast<const f32x16(&)[1][kTiles]>(acc);
         gemm_epilogue<E, 1>(args, whole, m0, n0, lane);
     } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            partial[wave][0][r][lane] = acc[0][r];
-            partial[wave][1][r][lane] = acc[1][r];
-        }
+        for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) partial[wave][j][r][lane] = acc[j][r];
         __syncthreads();
         const int j = lane & 31;
 #pragma unroll
         for (int u = 0; u < 16 / kParts; ++u) {
             const int r = (16 / kParts) * part + u;
-            float lo = partial[row_tile][0][r][lane], hi = partial[row_tile][1][r][lane];
+            float lo = partial[row_tile][0][r][lane], hi = partial[row_tile][kTiles - 1][r][lane];
 #pragma unroll
             for (int p = 1; p < kParts; ++p) {
                 lo += partial[row_tile + RT * p][0][r][lane];
-                hi += partial[row_tile + RT * p][1][r][lane];
+                hi += partial[row_tile + RT * p][kTiles - 1][r][lane];
             }
             if constexpr (kNorm) {
                 const float inv = row_scale(mfma32_row(lane, r));
@@ -719,7 +743,9 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
                 hi *= inv;
             }
             const int64_t out_row = m0 + mfma32_row(lane, r);
-            if (out_row < args.m) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
+            if (out_row >= args.m) continue;
+            if constexpr (kCols == 64) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
+            else gemm_store_one<E>(args, out_row, n0 + j, lo);
         }
     }
 }
@@ -1271,60 +1297,78 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 constexpr int64_t kRingBlocks = 256;
 constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
 
-// Row tiles per block of gemm_split_kernel for this GEMM, or 0 when it does not take it: the
-// smallest tiling whose grid fits the device once, for K = 576 (hidden) or 1536
-// (intermediate).  Shapes the 64 x 64 tile kernel takes use one row tile only: with more,
-// their 9 column tiles leave too many CUs idle (measured slower at 1024 to 2048 rows).
-static int split_row_tiles(const GemmArgs& args, GemmEpilogue epilogue) {
-    if (args.k != kHidden && args.k != kInter) return 0;
-    const bool narrow_shape = (epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) &&
-                              args.n % kBN != 0 && args.k % 32 == 0;
+// Tiling of gemm_split_kernel for this GEMM (rt = 0 when it does not take it), for K = 576
+// (hidden) or 1536 (intermediate), while the grid fits the device once.  Plain and residual
+// epilogues first try 32-column tiles (one row tile per block).  Otherwise 64-column tiles
+// with the smallest row tiling that fits; shapes the 64 x 64 tile kernel takes use one row
+// tile only: with more, their 9 column tiles leave too many CUs idle (measured slower at
+// 1024 to 2048 rows).
+struct SplitShape {
+    int rt;
+    int cols;
+};
+static SplitShape split_shape(const GemmArgs& args, GemmEpilogue epilogue) {
+    if (args.k != kHidden && args.k != kInter) return {0, 0};
+    const bool plain = epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual;
+    if (plain && (args.n / 32) * ((args.m + 31) / 32) <= kSplitBlocks) return {1, 32};
+    const bool narrow_shape = plain && args.n % kBN != 0 && args.k % 32 == 0;
     for (int rt = 1; rt <= (narrow_shape ? 1 : 4); rt *= 2)
-        if ((args.n / 64) * ((args.m + 32 * rt - 1) / (32 * rt)) <= kSplitBlocks) return rt;
-    return 0;
+        if ((args.n / 64) * ((args.m + 32 * rt - 1) / (32 * rt)) <= kSplitBlocks) return {rt, 64};
+    return {0, 0};
 }
 
 // gemm_split_kernel folds an RMSNorm of the A rows into the QKV and gate/up GEMMs (K = hidden).
 static bool split_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) {
     return args.k == kHidden && (epilogue == GemmEpilogue::kQkvRope || epilogue == GemmEpilogue::kSwiglu) &&
-           split_row_tiles(args, epilogue) != 0;
+           split_shape(args, epilogue).rt != 0;
 }
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
-    const int rt = split_row_tiles(args, epilogue);
+    const SplitShape shape = split_shape(args, epilogue);
+    const int rt = shape.rt;
     const bool norm = args.norm_weight != nullptr;
     if (norm && !split_folds_norm(args, epilogue)) return hipErrorInvalidValue;
     if (rt != 0) {
         const bool hidden = args.k == kHidden;
-        const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
+        const dim3 grid(static_cast<unsigned>(args.n / shape.cols),
+                        static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
         const dim3 split_block(64 * kSplitWaves);
-#define FLUX_SPLIT_RT(E, ST, RT, NORM)                                                                  \
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT, NORM>), grid, split_block, 0, stream, args)
+#define FLUX_SPLIT_RT(E, ST, RT, NORM, COLS)                                                                          \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT, NORM, COLS>), grid, split_block, 0, stream, \
+                       args)
 #define FLUX_LAUNCH_SPLIT(E)                                                                            \
     do {                                                                                                \
         if (rt == 1) {                                                                                  \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 1, false); else FLUX_SPLIT_RT(E, 24, 1, false);             \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 1, false, 64); else FLUX_SPLIT_RT(E, 24, 1, false, 64);     \
         } else if (rt == 2) {                                                                           \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 2, false); else FLUX_SPLIT_RT(E, 24, 2, false);             \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 2, false, 64); else FLUX_SPLIT_RT(E, 24, 2, false, 64);     \
         } else {                                                                                        \
-            if (hidden) FLUX_SPLIT_RT(E, 9, 4, false); else FLUX_SPLIT_RT(E, 24, 4, false);             \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 4, false, 64); else FLUX_SPLIT_RT(E, 24, 4, false, 64);     \
+        }                                                                                               \
+    } while (0)
+#define FLUX_LAUNCH_SPLIT_PLAIN(E)                                                                      \
+    do {                                                                                                \
+        if (shape.cols == 32) {                                                                         \
+            if (hidden) FLUX_SPLIT_RT(E, 9, 1, false, 32); else FLUX_SPLIT_RT(E, 24, 1, false, 32);     \
+        } else {                                                                                        \
+            FLUX_LAUNCH_SPLIT(E);                                                                       \
         }                                                                                               \
     } while (0)
 #define FLUX_LAUNCH_SPLIT_NORM(E)                                                                       \
     do {                                                                                                \
-        if (rt == 1) FLUX_SPLIT_RT(E, 9, 1, true);                                                      \
-        else if (rt == 2) FLUX_SPLIT_RT(E, 9, 2, true);                                                 \
-        else FLUX_SPLIT_RT(E, 9, 4, true);                                                              \
+        if (rt == 1) FLUX_SPLIT_RT(E, 9, 1, true, 64);                                                  \
+        else if (rt == 2) FLUX_SPLIT_RT(E, 9, 2, true, 64);                                             \
+        else FLUX_SPLIT_RT(E, 9, 4, true, 64);                                                          \
     } while (0)
         switch (epilogue) {
             case GemmEpilogue::kStore:
-                FLUX_LAUNCH_SPLIT(GemmEpilogue::kStore);
+                FLUX_LAUNCH_SPLIT_PLAIN(GemmEpilogue::kStore);
                 break;
             case GemmEpilogue::kResidual:
-                FLUX_LAUNCH_SPLIT(GemmEpilogue::kResidual);
+                FLUX_LAUNCH_SPLIT_PLAIN(GemmEpilogue::kResidual);
                 break;
             case GemmEpilogue::kSwiglu:
                 if (norm) FLUX_LAUNCH_SPLIT_NORM(GemmEpilogue::kSwiglu);
@@ -1335,6 +1379,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
                 else FLUX_LAUNCH_SPLIT(GemmEpilogue::kQkvRope);
                 break;
         }
+#undef FLUX_LAUNCH_SPLIT_PLAIN
 #undef FLUX_LAUNCH_SPLIT_NORM
 #undef FLUX_LAUNCH_SPLIT
 #undef FLUX_SPLIT_RT

@@ -246,11 +246,12 @@ def test_lm_head_argmax(gpu_device, vocab):
                                    (512, 576, 1536), (600, 1024, 576), (1200, 1024, 576), (1000, 576, 1536),
                                    (2048, 576, 1536), (300, 1024, 64), (300, 576, 64), (1024, 3072, 576)])
 def test_mfma_linear(gpu_device, m, n, k):
-    # k = 576 or 1536 with at most 256 tiles of (32 RT) x 64: the split kernel, RT = 1 (130 to
-    # 512 rows), 2 (600 rows) or 4 (1200 rows); widths that are not a multiple of 128 only with
-    # RT = 1. Otherwise those widths take the 64 x 64 tile kernel when k % 32 == 0 (1000, 2048
-    # rows), else the 128-column kernel; grids under 256 blocks take their four-buffer ring
-    # variants (300 rows with k = 64, 1000 rows, and the first three cases).
+    # k = 576 or 1536 with at most 256 tiles: the split kernel, on 32 x 32 tiles (130, 257 rows),
+    # else on (32 RT) x 64 tiles with RT = 1 (512 rows), 2 (600 rows) or 4 (1200 rows); widths
+    # that are not a multiple of 128 only with RT = 1. Otherwise those widths take the 64 x 64
+    # tile kernel when k % 32 == 0 (1000, 2048 rows), else the 128-column kernel; grids under 256
+    # blocks take their four-buffer ring variants (300 rows with k = 64, 1000 rows, and the
+    # first three cases).
     a = _randn(m, k, seed=61).to(gpu_device)
     w = _randn(n, k, seed=62, std=0.05).to(gpu_device)
     r = _randn(m, n, seed=63).to(gpu_device)
