@@ -322,12 +322,12 @@ int flux_qkv_rope_cache_rows_f32(const float* x, const float* packed_qkv, const 
 
 /* Workspace (bytes) flux_prefill_attention_f32 needs for a prompt of `seq` tokens: the
  * split-key partials of the 128-query tiles that see more than one key chunk (chunks of
- * 128 to 1536 keys, longer for longer prompts); 0 for seq <= 128.  Counterpart of the
+ * 128 to 1024 keys, longer for longer prompts); 0 for seq <= 128.  Counterpart of the
  * reference's partition workspace size (test_streaming_prefill_gqa.cu:503-512). */
 int flux_prefill_attention_workspace_bytes(int64_t seq, int64_t* bytes);
 
 /* Causal GQA prefill attention (FP32 MFMA, online softmax, keys split in chunks of
- * 128 to 1536 and merged): q [9,seq,64], K/V [3,capacity,64] -> out_rows [seq, 576].
+ * 128 to 1024 and merged): q [9,seq,64], K/V [3,capacity,64] -> out_rows [seq, 576].
  * `workspace` may be NULL when flux_prefill_attention_workspace_bytes reports 0.
  * Every pointer must be 16-byte aligned.
  * Replaces streaming_prefill_gqa_cuda_fp32 (csrc/streaming_prefill_gqa/

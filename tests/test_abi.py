@@ -91,9 +91,9 @@ def test_shape_constraints_are_rejected():
     # x 128 rows x (64 + m + l + 2 pad) floats
     assert lib.flux_prefill_attention_workspace_bytes(2048, ctypes.byref(size)) == _native.FLUX_OK
     assert size.value == 14 * 9 * 8 * 128 * 68 * 4
-    # 8192 tokens: 24-tile (1536-key) chunks, 52 query tiles past the first 12, 6 chunks
+    # 8192 tokens: 16-tile (1024-key) chunks, 56 query tiles past the first 8, 8 chunks
     assert lib.flux_prefill_attention_workspace_bytes(8192, ctypes.byref(size)) == _native.FLUX_OK
-    assert size.value == 52 * 9 * 6 * 128 * 68 * 4
+    assert size.value == 56 * 9 * 8 * 128 * 68 * 4
     dummy = ctypes.c_void_p(16)
     assert lib.flux_prefill_attention_f32(dummy, dummy, dummy, 4096, 4096, 0.125, None, dummy,
                                           None) == _native.FLUX_ERROR_INVALID_VALUE

@@ -318,7 +318,7 @@ def _attention_workspace(seq, device):
 @pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024),
                                           (1537, 1600), (2049, 2100), (3201, 3300), (4160, 4160)])
 def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
-    # Keys are split into chunks of 2 (up to 1024 tokens) to 24 (from about 5600 tokens on)
+    # Keys are split into chunks of 2 (up to 1024 tokens) to 16 (from about 4500 tokens on)
     # 64-key tiles; from 129 tokens on some query tiles see several chunks and take the
     # split-key path and its merge (1024: 2-tile chunks, eight of them, 3201: 10-tile chunks,
     # six of them, and a one-query last tile).
