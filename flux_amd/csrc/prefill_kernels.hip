@@ -1230,6 +1230,7 @@ prefill_attention_kernel(const float* __restrict__ q, const float* __restrict__ 
 // Combines the chunk partials of query tiles with more than one chunk.  Block
 // ((qt - attn_long_tile(seq)) * 9 + h) * 8 + row group; thread t -> row 16 * group + t / 16,
 // dims 4 (t % 16) .. + 3.  All chunk loads of a thread are issued before the combine.
+template <int kMaxChunks>
 __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(const float* __restrict__ workspace,
                                                                                int64_t seq,
                                                                                float* __restrict__ out_rows) {
@@ -1243,10 +1244,10 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(c
     const int64_t q0 = qt * kQTile;
     if (q0 + row >= seq) return;
     const int chunks = static_cast<int>(attn_chunks(seq, qt));
-    float4 o[kMergeMaxChunks];
-    float m[kMergeMaxChunks], l[kMergeMaxChunks];
+    float4 o[kMaxChunks];
+    float m[kMaxChunks], l[kMaxChunks];
 #pragma unroll
-    for (int c = 0; c < kMergeMaxChunks; ++c) {
+    for (int c = 0; c < kMaxChunks; ++c) {
         if (c < chunks) {
             const float* p = workspace + (attn_partial_slot(seq, qt, h, c) * kQTile + row) * kPartialRow;
             o[c] = *reinterpret_cast<const float4*>(p + d);
@@ -1261,11 +1262,11 @@ __global__ void __launch_bounds__(kAttnThreads) prefill_attention_merge_kernel(c
     }
     float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < kMergeMaxChunks; ++c) M = fmaxf(M, m[c]);
+    for (int c = 0; c < kMaxChunks; ++c) M = fmaxf(M, m[c]);
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kMergeMaxChunks; ++c) {
+    for (int c = 0; c < kMaxChunks; ++c) {
         const float f = fast_exp2(m[c] - M);
         O.x = fmaf(o[c].x, f, O.x);
         O.y = fmaf(o[c].y, f, O.y);
@@ -1476,9 +1477,18 @@ hipError_t launch_prefill_attention(const float* q, const float* key_cache, cons
     if (st != hipSuccess) return st;
     const int64_t long_tiles = attn_q_tiles(seq) - attn_long_tile(seq);
     if (long_tiles > 0 && attn_max_chunks(seq) > 1) {
-        hipLaunchKernelGGL(prefill_attention_merge_kernel,
-                           dim3(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / (kAttnThreads / 16)))),
-                           dim3(kAttnThreads), 0, stream, workspace, seq, out_rows);
+        // Registers for at most 4, 8 or 16 chunks: fewer registers, more waves in flight.
+        const dim3 grid(static_cast<unsigned>(long_tiles * kQHeads * (kQTile / (kAttnThreads / 16))));
+        const int64_t chunks = attn_max_chunks(seq);
+        if (chunks <= 4)
+            hipLaunchKernelGGL(prefill_attention_merge_kernel<4>, grid, dim3(kAttnThreads), 0, stream, workspace, seq,
+                               out_rows);
+        else if (chunks <= 8)
+            hipLaunchKernelGGL(prefill_attention_merge_kernel<8>, grid, dim3(kAttnThreads), 0, stream, workspace, seq,
+                               out_rows);
+        else
+            hipLaunchKernelGGL(prefill_attention_merge_kernel<kMergeMaxChunks>, grid, dim3(kAttnThreads), 0, stream,
+                               workspace, seq, out_rows);
         st = hipGetLastError();
     }
     return st;
