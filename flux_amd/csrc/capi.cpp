@@ -163,6 +163,18 @@ int flux_decode_device_error(flux_decode* runtime, int32_t* out) {
     return guarded([&] { *out = runtime->impl->device_error(); });
 }
 
+int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks) {
+    if (runtime == nullptr) return invalid("flux_decode_set_wait_limit: null argument");
+    runtime->impl->set_wait_limit(ticks);
+    return FLUX_OK;
+}
+
+int flux_decode_cooperative_graph(const flux_decode* runtime, int32_t* out) {
+    if (runtime == nullptr || out == nullptr) return invalid("flux_decode_cooperative_graph: null argument");
+    *out = runtime->impl->cooperative_graph() ? 1 : 0;
+    return FLUX_OK;
+}
+
 void flux_decode_destroy(flux_decode* runtime) {
     if (runtime == nullptr || !runtime->owned) return;
     delete runtime->impl;

@@ -49,7 +49,11 @@ constexpr int kThreads = 512;
 constexpr int kWavesPerWG = kThreads / kWave;
 constexpr int kAttnRows = 224;            // attention rows per workgroup (LDS-resident K/V)
 constexpr int kLmBatch = 4;
-constexpr uint64_t kTimeoutTicks = 20ull * 1000 * 1000;  // 200 ms of the 100 MHz wall clock
+// A wait that has lasted this long also watches the device error word, so one
+// workgroup's timeout ends every other workgroup's wait at once instead of
+// each of them timing out in turn (20 us of the 100 MHz wall clock; normal
+// exchanges complete in 1-10 us and never reach it).
+constexpr uint64_t kWatchErrorTicks = 2000;
 
 // ---------------------------------------------------------------------------
 // LL word helpers.
@@ -65,16 +69,48 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Bounded waiting.  A workgroup whose wait exceeds the timeout records an error
-// and stops waiting for the rest of the launch, so a bug can never hang the GPU.
-struct WaitCtx {
-    int* abort;        // LDS flag shared by the workgroup
-    int32_t* error;    // global error word
+// Bounded waiting.  A workgroup whose wait exceeds the limit records an error
+// (device word and its host-visible copy) and stops waiting for the rest of the
+// launch, so a bug can never hang the GPU; a wait that sees the device error word
+// set stops too.  Outputs of such a launch are invalid: the greedy token of every
+// step it finishes is written as -1.  The rarely used parts (host word, limit) sit
+// in LDS so that the waits keep no extra registers live.
+struct WaitShared {
+    int32_t* host_error;  // host-visible error word (mapped pinned memory)
+    uint64_t limit;       // wait bound in wall-clock ticks
 };
 
-__device__ __noinline__ void ll_timeout(int* abort, int32_t* error) {
+struct WaitCtx {
+    int* abort;                // LDS flag shared by the workgroup
+    int32_t* error;            // device error word
+    const WaitShared* shared;  // LDS
+};
+
+__device__ __noinline__ void record_error(int32_t* error, int32_t* host_error, int32_t code) {
+    __hip_atomic_store(error, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(host_error, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __noinline__ void ll_timeout(int* abort, int32_t* error, const WaitShared* shared) {
     *abort = 1;
-    __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    record_error(error, shared->host_error, 1);
+}
+
+// true when the wait must stop: the workgroup already aborted, the device error
+// word is set (checked once the wait is long), or the wait exceeded its bound.
+__device__ __forceinline__ bool wait_expired(const WaitCtx& w, uint64_t start) {
+    if (*w.abort) return true;
+    const uint64_t waited = wall_clock64() - start;
+    if (waited > kWatchErrorTicks &&
+        __hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+        *w.abort = 1;
+        return true;
+    }
+    if (waited > w.shared->limit) {
+        ll_timeout(w.abort, w.error, w.shared);
+        return true;
+    }
+    return false;
 }
 
 template <int N>
@@ -114,10 +150,7 @@ __device__ __forceinline__ void ll_fetch(const uint64_t* __restrict__ base, cons
                 ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
             }
             if (ready) break;
-            if (wall_clock64() - start > kTimeoutTicks) {
-                ll_timeout(w.abort, w.error);
-                break;
-            }
+            if (wait_expired(w, start)) break;
         }
     }
 #pragma unroll
@@ -758,6 +791,8 @@ __device__ __forceinline__ LayerWeights uniform_desc(const LayerWeights& d) {
 // Requires gridDim.x * 8 >= 1536 (one unit per wave in every phase).
 __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs args) {
     __shared__ int abort_flag;
+    __shared__ WaitShared wait_shared;
+    __shared__ int32_t step_error;
     __shared__ LayerWeights layer_desc[kLayers];
     __shared__ float red[kAttnRedFloats];
     __shared__ __align__(16) float attn_sp[kAttnSpFloats];
@@ -781,23 +816,26 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     const int64_t layer_stride = kKVHeads * head_stride;
     const int partial_stride = kGroup * (kHeadDim + 2);
 
-    if (tid_opaque() == 0) abort_flag = 0;
+    if (tid_opaque() == 0) {
+        abort_flag = 0;
+        wait_shared = WaitShared{args.host_error, args.wait_ticks};
+    }
     if (tid_opaque() < kLayers) layer_desc[tid_opaque()] = args.layers[tid_opaque()];
     const uint32_t counter0 = *args.token_counter;
     int64_t token = *args.input_token;
     int64_t position = *args.position;
     int64_t step = *args.generation_step;
     __syncthreads();
-    const WaitCtx wctx{&abort_flag, args.error};
+    const WaitCtx wctx{&abort_flag, args.error, &wait_shared};
 
-    for (int t = 0; t < args.steps; ++t) {
+    int t = 0;
+    for (; t < args.steps; ++t) {
         __syncthreads();
         const bool stop = abort_flag != 0;
         __syncthreads();
         if (stop) break;
         if (position < 0 || position >= cap) {
-            if (wg == 0 && tid_opaque() == 0)
-                __hip_atomic_store(args.error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (wg == 0 && tid_opaque() == 0) record_error(args.error, wait_shared.host_error, 2);
             break;
         }
         const uint32_t counter = counter0 + static_cast<uint32_t>(t);
@@ -1045,6 +1083,10 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             int64_t best_i = INT64_MAX;
             lm_rows_pipelined(args.lm_head, x, wl, row0, row1, lane, LogitsPlainOut{args.logits}, best_v, best_i);
             wg_argmax(best_v, best_i, red_v, red_i);
+            // WG 0 reads the device error word before the argmax exchange; it decides below
+            // whether this step's token is valid, by which time the load has returned.
+            if (wg == 0 && tid_opaque() == 0)
+                step_error = __hip_atomic_load(args.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             FLUX_TRACE_POINT(2);
             // This token's K/V cache rows were written through (agent-scope stores); wait
             // until every wave's stores are acknowledged before signalling the argmax.  The
@@ -1080,8 +1122,12 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             __syncthreads();
             const int64_t next = token_shared;
             if (wg == 0 && tid_opaque() == 0) {
-                *args.input_token = next;
-                if (step >= 0 && step < args.generated_capacity) args.generated[step] = next;
+                // A step that ran after any workgroup's wait gave up computed from stale
+                // inputs: its token is reported as -1, never as a plausible id.
+                const bool failed = step_error != 0 || abort_flag != 0;
+                const int64_t reported = failed ? int64_t{-1} : next;
+                *args.input_token = reported;
+                if (step >= 0 && step < args.generated_capacity) args.generated[step] = reported;
                 *args.generation_step = step + 1;
                 *args.position = attended;
                 *args.cache_length = attended;
@@ -1092,7 +1138,18 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         }
     }
     __syncthreads();
-    if (wg == 0 && tid_opaque() == 0) *args.token_counter = counter0 + static_cast<uint32_t>(args.steps);
+    if (wg == 0 && tid_opaque() == 0) {
+        // A launch that ended early reports token -1 for the steps it did not compute, so
+        // no earlier generation's tokens stay in those slots looking valid.
+        if (t < args.steps) {
+            for (int r = t; r < args.steps; ++r) {
+                const int64_t slot = step + (r - t);
+                if (slot >= 0 && slot < args.generated_capacity) args.generated[slot] = -1;
+            }
+            *args.input_token = -1;
+        }
+        *args.token_counter = counter0 + static_cast<uint32_t>(args.steps);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1286,10 +1343,12 @@ __global__ void __launch_bounds__(kThreads) argmax_finish_kernel(const float* pa
 
 // Scalar state installation (no host-pageable async copies, graph-safe):
 // input_token = *token_src, position = cache_length = position_value,
-// generation_step = step_value, and generated[0] = token when requested.
+// generation_step = step_value, and generated[0] = token when requested; the
+// device and host-visible error words (when given) are cleared.
 __global__ void install_state_kernel(const int64_t* token_src, int64_t position_value, int64_t step_value,
                                      int write_generated0, int64_t* input_token, int64_t* position,
-                                     int64_t* cache_length, int64_t* step, int64_t* generated) {
+                                     int64_t* cache_length, int64_t* step, int64_t* generated, int32_t* error,
+                                     int32_t* host_error) {
     if (tid_opaque() != 0) return;
     const int64_t token = *token_src;
     *input_token = token;
@@ -1297,6 +1356,8 @@ __global__ void install_state_kernel(const int64_t* token_src, int64_t position_
     *cache_length = position_value;
     *step = step_value;
     if (write_generated0) generated[0] = token;
+    if (error != nullptr) __hip_atomic_store(error, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (host_error != nullptr) __hip_atomic_store(host_error, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 }  // namespace
@@ -1325,10 +1386,17 @@ int max_attention_positions(int grid) {
     return chunks * kAttnRows;
 }
 
+// Cooperative launch: the runtime refuses to start a grid whose workgroups cannot all be
+// resident at once (hipErrorCooperativeLaunchTooLarge), instead of letting the resident
+// ones wait for the rest until their bounded waits expire.
 hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL(fused_decode_kernel, dim3(grid), dim3(kThreads), fused_decode_dynamic_lds(), stream, args);
-    return hipGetLastError();
+    DecodeArgs copy = args;
+    void* params[] = {&copy};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fused_decode_kernel), dim3(grid), dim3(kThreads),
+                                      params, static_cast<unsigned int>(fused_decode_dynamic_lds()), stream);
 }
+
+void* fused_decode_function() { return reinterpret_cast<void*>(fused_decode_kernel); }
 
 hipError_t fused_decode_occupancy(int* blocks_per_cu) {
     hipError_t st = hipFuncSetAttribute(reinterpret_cast<const void*>(fused_decode_kernel),
@@ -1405,9 +1473,11 @@ hipError_t launch_argmax(const float* logits, int64_t n, int64_t* token, int64_t
 
 hipError_t launch_install_state(const int64_t* token_src, int64_t position_value, int64_t step_value,
                                 bool write_generated0, int64_t* input_token, int64_t* position, int64_t* cache_length,
-                                int64_t* step, int64_t* generated, hipStream_t stream) {
+                                int64_t* step, int64_t* generated, int32_t* error, int32_t* host_error,
+                                hipStream_t stream) {
     hipLaunchKernelGGL(install_state_kernel, dim3(1), dim3(64), 0, stream, token_src, position_value, step_value,
-                       write_generated0 ? 1 : 0, input_token, position, cache_length, step, generated);
+                       write_generated0 ? 1 : 0, input_token, position, cache_length, step, generated, error,
+                       host_error);
     return hipGetLastError();
 }
 

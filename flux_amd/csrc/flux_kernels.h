@@ -29,7 +29,9 @@ struct DecodeArgs {
     int64_t* cache_length;
     uint64_t* ll;                // LL arena (ll_arena_words())
     uint32_t* token_counter;
-    int32_t* error;
+    int32_t* error;              // device error word (0 = none)
+    int32_t* host_error;         // host-visible copy of the error word (mapped pinned memory)
+    uint64_t wait_ticks;         // bound of every cross-workgroup wait (100 MHz wall clock)
     int64_t capacity;
     int64_t vocab;
     int64_t generated_capacity;
@@ -43,6 +45,7 @@ size_t fused_decode_dynamic_lds();
 int max_attention_positions(int grid);
 hipError_t fused_decode_occupancy(int* blocks_per_cu);
 hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream);
+void* fused_decode_function();
 
 // ---- isolated decode phases ----
 hipError_t launch_qkv_rope_cache(const float* hidden, const float* norm_w, float eps, const float* qkv_w,
@@ -67,7 +70,8 @@ hipError_t launch_argmax(const float* logits, int64_t n, int64_t* token, int64_t
                          hipStream_t stream);
 hipError_t launch_install_state(const int64_t* token_src, int64_t position_value, int64_t step_value,
                                 bool write_generated0, int64_t* input_token, int64_t* position, int64_t* cache_length,
-                                int64_t* step, int64_t* generated, hipStream_t stream);
+                                int64_t* step, int64_t* generated, int32_t* error, int32_t* host_error,
+                                hipStream_t stream);
 // *position += 1 (one thread; the layer runtime's step epilogue).
 hipError_t launch_advance_position(int64_t* position, hipStream_t stream);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows, int cols, float eps,

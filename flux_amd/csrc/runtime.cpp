@@ -84,6 +84,15 @@ void validate_scalars(const double* epsilons, const double* scales, const char* 
     }
 }
 
+std::string device_error_message(int32_t err) {
+    return "flux native full decode: device-side error " + std::to_string(err) +
+           (err == 1 ? " (cross-workgroup wait timed out; the steps it affected report token -1)"
+                     : " (position outside capacity)");
+}
+
+// Default bound of every cross-workgroup wait of the fused decode kernel: 200 ms.
+constexpr uint64_t kDefaultWaitTicks = 20ull * 1000 * 1000;
+
 int decode_grid() {
     const int cus = device_cu_count();
     int blocks = 0;
@@ -168,8 +177,8 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
 
         args_ = DecodeArgs{layers_, weights.embedding, weights.lm_head, weights.final_norm, final_eps_,
                            rope_cos_, rope_sin_, key_cache_, value_cache_, logits_, input_token_, generated_,
-                           generation_step_, position_, cache_length_, ll_, token_counter_, error_, capacity_,
-                           vocab_, capacity_, 1};
+                           generation_step_, position_, cache_length_, ll_, token_counter_, error_,
+                           host_error_device_, kDefaultWaitTicks, capacity_, vocab_, capacity_, 1};
 
         check_hip(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking), "creating capture stream");
         check_hip(hipEventCreateWithFlags(&completion_, hipEventDisableTiming), "creating completion event");
@@ -187,14 +196,37 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
         initialize_state(initial_token, sources, position, capture_stream_, true);
         check_hip(counted_stream_sync(capture_stream_), "initialising decode state");
 
-        // Capture one token step (a single fused-kernel node) for replay().
+        // Capture one token step (a single fused-kernel node) for replay(), then mark the
+        // node cooperative so that a replay whose grid cannot be co-resident fails at
+        // launch; where the runtime cannot mark it, the node keeps a plain launch and the
+        // occupancy check above plus the bounded waits remain the guard.
         check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
-        hipError_t launch_status = launch_fused_decode(args_, grid_, capture_stream_);
+        DecodeArgs capture_args = args_;
+        void* params[] = {&capture_args};
+        hipError_t launch_status =
+            hipLaunchKernel(fused_decode_function(), dim3(grid_), dim3(fused_decode_threads()), params,
+                            fused_decode_dynamic_lds(), capture_stream_);
         hipGraph_t graph = nullptr;
         hipError_t end_status = hipStreamEndCapture(capture_stream_, &graph);
         graph_ = graph;
         check_hip(launch_status, "capturing fused decode step");
         check_hip(end_status, "ending graph capture");
+        {
+            size_t count = 0;
+            check_hip(hipGraphGetNodes(graph_, nullptr, &count), "counting graph nodes");
+            std::vector<hipGraphNode_t> nodes(count);
+            if (count > 0) check_hip(hipGraphGetNodes(graph_, nodes.data(), &count), "listing graph nodes");
+            for (hipGraphNode_t node : nodes) {
+                hipGraphNodeType type;
+                check_hip(hipGraphNodeGetType(node, &type), "reading graph node type");
+                if (type != hipGraphNodeTypeKernel) continue;
+                hipLaunchAttributeValue value{};
+                value.cooperative = 1;
+                cooperative_graph_ =
+                    hipGraphKernelNodeSetAttribute(node, hipKernelNodeAttributeCooperative, &value) == hipSuccess;
+                (void)hipGetLastError();
+            }
+        }
         check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating decode graph");
         check_hip(counted_stream_sync(capture_stream_), "finalising capture");
     } catch (...) {
@@ -219,11 +251,13 @@ void DecodeRuntime::release() noexcept {
     }
     if (cache_block_) (void)counted_free(cache_block_);
     if (state_block_) (void)counted_free(state_block_);
+    if (host_error_) (void)hipHostFree(host_error_);
     graph_exec_ = nullptr;
     graph_ = nullptr;
     completion_ = nullptr;
     capture_stream_ = nullptr;
     cache_block_ = state_block_ = nullptr;
+    host_error_ = host_error_device_ = nullptr;
     if (previous >= 0 && previous != device_) (void)hipSetDevice(previous);
 }
 
@@ -263,6 +297,19 @@ void DecodeRuntime::allocate() {
     error_ = reinterpret_cast<int32_t*>(base + o_error);
     layers_ = reinterpret_cast<LayerWeights*>(base + o_layers);
     ll_ = reinterpret_cast<uint64_t*>(base + o_ll);
+    // The kernel's error word also lands in mapped pinned host memory, so every runtime call
+    // can see a finished launch's device error without synchronising.
+    check_hip(hipHostMalloc(reinterpret_cast<void**>(&host_error_), sizeof(int32_t),
+                            hipHostMallocMapped | hipHostMallocCoherent),
+              "allocating the host-visible error word");
+    *host_error_ = 0;
+    check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&host_error_device_), host_error_, 0),
+              "mapping the host-visible error word");
+}
+
+void DecodeRuntime::check_host_error() const {
+    const int32_t err = __atomic_load_n(host_error_, __ATOMIC_ACQUIRE);
+    if (err != 0) throw FluxError(FLUX_ERROR_DEVICE, device_error_message(err));
 }
 
 void DecodeRuntime::initialize_state(const int64_t* token, const CacheSources& sources, int64_t position,
@@ -285,7 +332,7 @@ void DecodeRuntime::initialize_state(const int64_t* token, const CacheSources& s
         }
     }
     check_hip(launch_install_state(token, position, 0, false, input_token_, position_, cache_length_, generation_step_,
-                                   generated_, stream),
+                                   generated_, error_, host_error_device_, stream),
               "initialising device state");
     if (clear_outputs) {
         check_hip(hipMemsetAsync(logits_, 0, sizeof(float) * vocab_, stream), "clearing logits");
@@ -294,6 +341,7 @@ void DecodeRuntime::initialize_state(const int64_t* token, const CacheSources& s
 }
 
 float* DecodeRuntime::replay(const int64_t* token, hipStream_t stream) {
+    check_host_error();
     if (replay_count_ >= capacity_ - start_position_)
         bad_state("flux native full decode: fixed-capacity state is exhausted");
     check_hip(hipSetDevice(device_), "hipSetDevice");
@@ -324,6 +372,7 @@ int64_t* DecodeRuntime::generate_greedy(int64_t decode_steps, hipStream_t stream
     if (decode_steps > capacity_ - start_position_ - replay_count_)
         bad_state("flux native full decode: fixed-capacity generation is exhausted");
     if (generation_started_) bad_state("flux native full decode: prefill or reset is required before reuse");
+    check_host_error();
     check_hip(hipSetDevice(device_), "hipSetDevice");
     if (pending_) check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering greedy generation");
     if (decode_steps > 0) {
@@ -369,6 +418,7 @@ void DecodeRuntime::reset(const int64_t* token, const CacheSources& sources, int
     }
     initialize_state(token, sources, position, stream, true);
     check_hip(counted_stream_sync(stream), "resetting full runtime state");
+    *host_error_ = 0;
     start_position_ = position;
     replay_count_ = 0;
     generation_started_ = false;
@@ -384,8 +434,16 @@ void DecodeRuntime::wait_for_prefill(hipStream_t stream) {
 void DecodeRuntime::install_prefilled_state(const int64_t* token, int64_t position, hipStream_t stream) {
     if (position < 1 || position > capacity_)
         invalid("flux native full decode: prefill position must be in [1, capacity]");
+    // A prefill re-arms a runtime whose earlier launch reported a device error: the
+    // install kernel clears both error words in stream order; the host copy is also
+    // cleared here, once the failed launch has finished, so the next call does not
+    // see the stale word before the install kernel has run.
+    if (__atomic_load_n(host_error_, __ATOMIC_ACQUIRE) != 0) {
+        check_hip(counted_stream_sync(stream), "waiting for the failed decode launch");
+        *host_error_ = 0;
+    }
     check_hip(launch_install_state(token, position, 1, true, input_token_, position_, cache_length_, generation_step_,
-                                   generated_, stream),
+                                   generated_, error_, host_error_device_, stream),
               "installing prefilled state");
     check_hip(hipEventRecord(completion_, stream), "recording prefill completion");
     start_position_ = position;
@@ -401,10 +459,7 @@ int64_t DecodeRuntime::read_scalar(const int64_t* device_value) {
     check_hip(counted_memcpy(&result, device_value, sizeof(result), hipMemcpyDeviceToHost), "reading device state");
     int32_t err = 0;
     check_hip(counted_memcpy(&err, error_, sizeof(err), hipMemcpyDeviceToHost), "reading device error word");
-    if (err != 0)
-        throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: device-side error " + std::to_string(err) +
-                                               (err == 1 ? " (cross-workgroup wait timed out)"
-                                                         : " (position outside capacity)"));
+    if (err != 0) throw FluxError(FLUX_ERROR_DEVICE, device_error_message(err));
     return result;
 }
 

@@ -58,9 +58,16 @@ public:
     void buffers(flux_decode_buffers* out) const;
     void graph_nodes(int64_t* kernels, int64_t* total) const;
     int device() const { return device_; }
+    // Bound of every cross-workgroup wait of later generate_greedy launches, in 100 MHz
+    // wall-clock ticks (the captured replay graph keeps the bound it was captured with).
+    void set_wait_limit(uint64_t ticks) { args_.wait_ticks = ticks; }
+    bool cooperative_graph() const { return cooperative_graph_; }
 
 private:
     void allocate();
+    // Raises FluxError(FLUX_ERROR_DEVICE) when a finished launch reported a device-side
+    // error (non-blocking: reads the host-visible error word).
+    void check_host_error() const;
     void initialize_state(const int64_t* token, const CacheSources& sources, int64_t position, hipStream_t stream,
                           bool clear_outputs);
     void launch_steps(int64_t steps, hipStream_t stream, hipStream_t launch_stream);
@@ -93,6 +100,9 @@ private:
     uint64_t* ll_ = nullptr;
     uint32_t* token_counter_ = nullptr;
     int32_t* error_ = nullptr;
+    int32_t* host_error_ = nullptr;         // mapped pinned host memory
+    int32_t* host_error_device_ = nullptr;  // its device address
+    bool cooperative_graph_ = false;
     LayerWeights* layers_ = nullptr;
     size_t state_bytes_ = 0;
     size_t ll_bytes_ = 0;

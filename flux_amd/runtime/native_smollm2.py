@@ -109,22 +109,53 @@ def _rope_tables(model: nn.Module, length: int) -> tuple[torch.Tensor, torch.Ten
     return cos, sin
 
 
-def _model_weights(model: nn.Module) -> tuple[_native.FluxWeights, list[float], list[float]]:
+def _model_weight_tensors(model: nn.Module, device: torch.device) -> list[torch.Tensor]:
+    """Every weight the native runtimes read, each checked before its pointer crosses the C ABI.
+
+    The kernels read raw device pointers, so a tensor on another device, of another
+    dtype or shape, or with strides (a transposed or sliced view) would be read as
+    garbage or fault the GPU.  The reference checks each tensor the same way
+    (native_decode_runtime_cuda.cu:1108-1123, native_prefill_runtime_cuda.cu:460-482).
+    Returns, in order: embedding, lm_head, final norm, then per layer the input norm,
+    packed QKV, o_proj, post-attention norm, packed gate/up and down weights.
+    """
+    vocab = int(model.config.vocab_size)
     layers = list(model.model.layers)
-    weights = _native.weights_struct(
-        model.model.embed_tokens.weight,
-        model.lm_head.weight,
-        model.model.norm.weight,
-        [layer.input_layernorm.weight for layer in layers],
-        [layer.self_attn.packed_qkv.weight for layer in layers],
-        [layer.self_attn.o_proj.weight for layer in layers],
-        [layer.post_attention_layernorm.weight for layer in layers],
-        [layer.mlp.gate_up_proj.weight for layer in layers],
-        [layer.mlp.down_proj.weight for layer in layers],
-    )
+    named = [("embedding", model.model.embed_tokens.weight, (vocab, 576)),
+             ("lm_head", model.lm_head.weight, (vocab, 576)),
+             ("final norm", model.model.norm.weight, (576,))]
+    for i, layer in enumerate(layers):
+        named += [(f"layer {i} input norm", layer.input_layernorm.weight, (576,)),
+                  (f"layer {i} packed QKV", layer.self_attn.packed_qkv.weight, (960, 576)),
+                  (f"layer {i} o_proj", layer.self_attn.o_proj.weight, (576, 576)),
+                  (f"layer {i} post-attention norm", layer.post_attention_layernorm.weight, (576,)),
+                  (f"layer {i} packed gate/up", layer.mlp.gate_up_proj.weight, (3072, 576)),
+                  (f"layer {i} down", layer.mlp.down_proj.weight, (576, 1536))]
+    for name, tensor, shape in named:
+        if not isinstance(tensor, torch.Tensor):
+            raise ValueError(f"native SmolLM2 runtime: {name} weight is missing")
+        if tensor.device != device:
+            raise ValueError(f"native SmolLM2 runtime: {name} weight is on {tensor.device}, expected {device}")
+        if tensor.dtype != torch.float32:
+            raise ValueError(f"native SmolLM2 runtime: {name} weight has dtype {tensor.dtype}, expected float32")
+        if tuple(tensor.shape) != shape:
+            raise ValueError(f"native SmolLM2 runtime: {name} weight has shape {list(tensor.shape)}, "
+                             f"expected {list(shape)}")
+        if not tensor.is_contiguous():
+            raise ValueError(f"native SmolLM2 runtime: {name} weight must be contiguous")
+    return [tensor.detach() for _, tensor, _ in named]
+
+
+def _model_weights(model: nn.Module, device: torch.device
+                   ) -> tuple[_native.FluxWeights, list[float], list[float], tuple[torch.Tensor, ...]]:
+    """The C ABI weight struct, epsilons and attention scales, plus the tensors it borrows."""
+    tensors = _model_weight_tensors(model, device)
+    layers = list(model.model.layers)
+    per_layer = [tensors[3 + k::6] for k in range(6)]
+    weights = _native.weights_struct(tensors[0], tensors[1], tensors[2], *per_layer)
     epsilons = [float(layer.input_layernorm.variance_epsilon) for layer in layers]
     scales = [float(layer.self_attn.scaling) for layer in layers]
-    return weights, epsilons, scales
+    return weights, epsilons, scales, tuple(tensors)
 
 
 class _NativeAllocation:
@@ -227,6 +258,16 @@ class _DecodeHandle:
             _native.check(_native.load().flux_decode_device_error(self.raw, ctypes.byref(out)))
         return int(out.value)
 
+    def set_wait_limit(self, ticks: int) -> None:
+        """Bound (100 MHz ticks) of the cross-workgroup waits of later generate_greedy launches."""
+        _native.check(_native.load().flux_decode_set_wait_limit(self.raw, int(ticks)))
+
+    def cooperative_graph(self) -> bool:
+        """Whether the captured replay graph's kernel node is a cooperative launch."""
+        out = ctypes.c_int32()
+        _native.check(_native.load().flux_decode_cooperative_graph(self.raw, ctypes.byref(out)))
+        return bool(out.value)
+
 
 class _PrefillHandle:
     def __init__(self, raw: int, device: torch.device, keepalive: Any) -> None:
@@ -273,14 +314,16 @@ class NativeSmolLM2Prefill:
         self.input_ids = input_ids
         self._rope_cos = cos_cpu.to(device)
         self._rope_sin = sin_cpu.to(device)
-        weights, epsilons, scales = _model_weights(model)
+        weights, epsilons, scales, borrowed = _model_weights(model, device)
         raw = ctypes.c_void_p()
         with torch.cuda.device(device):
             _native.check(_native.load().flux_prefill_create(
                 ctypes.byref(weights), _native.ptr(self._rope_cos), _native.ptr(self._rope_sin), requested,
                 _native.ptr(input_ids), input_ids.shape[1], _native.double_array(epsilons),
                 _native.double_array(scales), _native.current_stream(device), ctypes.byref(raw)))
-        self._handle = _PrefillHandle(raw.value, device, keepalive=(model, self._rope_cos, self._rope_sin))
+        # The runtime borrows the weight storage: keep the tensors themselves alive (moving the
+        # model or reassigning a parameter's data afterwards does not free what it reads).
+        self._handle = _PrefillHandle(raw.value, device, keepalive=(borrowed, self._rope_cos, self._rope_sin))
         self.prefill_logits = self._handle.logits
         return self
 
@@ -449,7 +492,7 @@ class NativeSmolLM2Decode:
         self._rope_sin = sin_cpu.to(device)
         self._source_key_caches = tuple(key_caches)
         self._source_value_caches = tuple(value_caches)
-        weights, epsilons, scales = _model_weights(model)
+        weights, epsilons, scales, borrowed = _model_weights(model, device)
         raw = ctypes.c_void_p()
         with torch.cuda.device(device):
             _native.check(_native.load().flux_decode_create(
@@ -458,7 +501,7 @@ class NativeSmolLM2Decode:
                 _native.pointer_array(value_caches), _native.length_array([k.shape[2] for k in key_caches]),
                 _native.double_array(epsilons), _native.double_array(scales), _native.current_stream(device),
                 ctypes.byref(raw)))
-        owner = _NativeAllocation(raw.value, "flux_decode_destroy", (model, self._rope_cos, self._rope_sin))
+        owner = _NativeAllocation(raw.value, "flux_decode_destroy", (borrowed, self._rope_cos, self._rope_sin))
         self._handle = _DecodeHandle(raw.value, device, owner)
         self.prefill_logits = None
         self.prefill_input_ids = None

@@ -6,7 +6,8 @@ seeded random weights (there is no network to fetch a checkpoint):
 * Linear and Embedding weights ~ N(0, 0.02), RMSNorm weights = 1, which is the
   Hugging Face ``LlamaForCausalLM`` initialisation rule
   (transformers ``modeling_llama.py`` ``LlamaPreTrainedModel`` / ``LlamaRMSNorm``).
-* The embedding is tied to the LM head.
+* The embedding is tied to the LM head (``SyntheticSpec`` can untie it for the
+  token-feedback tests).
 * RoPE theta 1e5, RMSNorm eps 1e-5, 9 query heads, 3 KV heads, head_dim 64.
 
 Random numbers come from numpy's PCG64 ``standard_normal`` in float32, which is
@@ -42,10 +43,32 @@ MAX_POSITIONS = 16384
 
 @dataclass(frozen=True)
 class SyntheticSpec:
+    """Seed and shape of a synthetic model.
+
+    ``permuted_head_seed`` (optional) unties the LM head: it becomes a seeded row
+    permutation of the N(0, 0.02) embedding draw, and the input embedding is that
+    draw times ``embedding_scale``.  With a large scale the embedded token
+    dominates the final hidden state, so the greedy successor of token t is
+    ``argsort(perm)[t]`` (the LM-head row holding t's embedding) and the greedy
+    stream changes at every step -- a stream that exercises the on-device token
+    feedback, which the tied synthetic model (whose greedy stream settles on one
+    token) cannot.
+    """
+
     seed: int = 0
     vocab: int = VOCAB
     layers: int = LAYERS
     max_positions: int = MAX_POSITIONS
+    permuted_head_seed: int | None = None
+    embedding_scale: float = 1.0
+
+    @property
+    def tied(self) -> bool:
+        return self.permuted_head_seed is None
+
+
+# The untied model of the token-feedback tests.
+PERMUTED_HEAD_SPEC = SyntheticSpec(seed=0, permuted_head_seed=4242, embedding_scale=50.0)
 
 
 def _layer_keys(index: int) -> list[tuple[str, tuple[int, ...]]]:
@@ -64,7 +87,9 @@ def _layer_keys(index: int) -> list[tuple[str, tuple[int, ...]]]:
 def synthetic_state_dict(spec: SyntheticSpec = SyntheticSpec()) -> dict[str, torch.Tensor]:
     """Hugging Face Llama state dict (CPU float32) for the synthetic model.
 
-    ``lm_head.weight`` is the same tensor object as the embedding (tied).
+    ``lm_head.weight`` is the same tensor object as the embedding when the spec
+    is tied; otherwise it is the seeded row permutation described on
+    ``SyntheticSpec``.
     """
     rng = np.random.Generator(np.random.PCG64(spec.seed))
     std = np.float32(INIT_STD)
@@ -83,7 +108,13 @@ def synthetic_state_dict(spec: SyntheticSpec = SyntheticSpec()) -> dict[str, tor
         state[p + "input_layernorm.weight"] = torch.ones(HIDDEN)
         state[p + "post_attention_layernorm.weight"] = torch.ones(HIDDEN)
     state["model.norm.weight"] = torch.ones(HIDDEN)
-    state["lm_head.weight"] = state["model.embed_tokens.weight"]
+    if spec.tied:
+        state["lm_head.weight"] = state["model.embed_tokens.weight"]
+    else:
+        table = state["model.embed_tokens.weight"]
+        perm = np.random.Generator(np.random.PCG64(spec.permuted_head_seed)).permutation(spec.vocab)
+        state["lm_head.weight"] = table[torch.from_numpy(perm)].contiguous()
+        state["model.embed_tokens.weight"] = table * np.float32(spec.embedding_scale)
     return state
 
 
@@ -91,7 +122,7 @@ def weights_sha256(state: dict[str, torch.Tensor]) -> str:
     """SHA-256 over every tensor's bytes in sorted-key order (tied tensors once)."""
     digest = hashlib.sha256()
     for key in sorted(state):
-        if key == "lm_head.weight":
+        if key == "lm_head.weight" and state[key] is state["model.embed_tokens.weight"]:
             continue
         digest.update(key.encode())
         digest.update(state[key].contiguous().numpy().tobytes())
@@ -120,7 +151,7 @@ def llama_config(spec: SyntheticSpec = SyntheticSpec()):
         max_position_embeddings=spec.max_positions,
         rms_norm_eps=RMS_EPS,
         rope_parameters={"rope_type": "default", "rope_theta": ROPE_THETA},
-        tie_word_embeddings=True,
+        tie_word_embeddings=spec.tied,
         attention_bias=False,
         attention_dropout=0.0,
         mlp_bias=False,
@@ -141,7 +172,8 @@ def build_hf_model(spec: SyntheticSpec = SyntheticSpec(), device: str | torch.de
         model = LlamaForCausalLM(config)
     state = synthetic_state_dict(spec)
     model.load_state_dict(state, assign=True, strict=True)
-    model.tie_weights()
+    if spec.tied:
+        model.tie_weights()
     # Non-persistent buffers (RoPE inv_freq) are not in the state dict: rebuild them.
     rotary = type(model.model.rotary_emb)(config)
     model.model.rotary_emb = rotary

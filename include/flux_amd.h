@@ -126,11 +126,18 @@ int flux_decode_create(const flux_weights* weights, const float* rope_cos, const
                        const double* attention_scales, hipStream_t stream, flux_decode** out);
 
 /* One decode step: optional token copy (device [1,1] int64, may be NULL), then
- * graph replay; returns the logits buffer.  (native_decode_runtime_cuda.cu:907-931) */
+ * graph replay; returns the logits buffer.  (native_decode_runtime_cuda.cu:907-931)
+ * Like flux_decode_generate_greedy, it first returns FLUX_ERROR_DEVICE when an
+ * earlier launch that has finished reported a device-side error (non-blocking
+ * check of a host-visible error word); prefill or reset re-arms the runtime.
+ * The fused kernel needs every workgroup resident at once (one per CU): direct
+ * launches are cooperative and fail when that cannot hold; the GPU must not be
+ * shared with other work while a launch runs. */
 int flux_decode_replay(flux_decode* runtime, const int64_t* token, hipStream_t stream, float** logits);
 
 /* `decode_steps` greedy steps in one launch of the fused decode kernel; returns
- * the generated-token buffer.  (native_decode_runtime_cuda.cu:933-960) */
+ * the generated-token buffer.  (native_decode_runtime_cuda.cu:933-960)
+ * A step computed after a device-side error holds token -1. */
 int flux_decode_generate_greedy(flux_decode* runtime, int64_t decode_steps, hipStream_t stream,
                                 int64_t** generated_tokens);
 
@@ -149,6 +156,19 @@ int flux_decode_capacity(const flux_decode* runtime, int64_t* out);
 int flux_decode_get_buffers(const flux_decode* runtime, flux_decode_buffers* out);
 /* Wait for outstanding work and return the device error word (0 = none). */
 int flux_decode_device_error(flux_decode* runtime, int32_t* out);
+
+/* Bound, in 100 MHz wall-clock ticks, of every cross-workgroup wait of later
+ * flux_decode_generate_greedy launches (default 200 ms; the captured replay graph
+ * keeps the default).  A wait that exceeds it records device error 1; the steps it
+ * affects report token -1, and the next runtime call raises FLUX_ERROR_DEVICE.
+ * No counterpart in the reference: the failure-handling test sets a tiny bound to
+ * drive that path with every kernel still exiting normally. */
+int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks);
+
+/* *out = 1 when the captured replay graph's kernel node is a cooperative launch
+ * (its workgroups are guaranteed co-resident or the launch fails), else 0.
+ * No counterpart in the reference (its decode step is ordinary launches). */
+int flux_decode_cooperative_graph(const flux_decode* runtime, int32_t* out);
 /* Time the next `decode_steps` steps with events on `stream` (benchmark aid). */
 /* Nodes of the captured replay graph: kernel nodes (the launches per replay) and all
  * nodes.  Counterpart of the launch count the reference's runtime audit takes with

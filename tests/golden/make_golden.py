@@ -12,14 +12,31 @@ synthetic weights, and stores small vectors under ``tests/golden/``:
 * ``config1.npz``       config 1: 128-token prompt, 32 greedy tokens, per-step
                         top-64 logits, a fixed 256-index logit probe, top-2 margins,
                         and K/V slices after the prompt.
-* ``ctx{N}.npz``        prompts of N tokens (512 / 1024 / 2048 / 8192), greedy
-                        continuation with the same per-step probes.
+* ``ctx{N}.npz``        config 2: prompts of N tokens (128 / 512 / 1024 / 2048 / 4096 /
+                        8192) and 128 greedy tokens (513 at 8192: config 5 reaches
+                        position 8704).  Every step keeps the token, the top-2 margin
+                        and the top-8 logits; the steps in ``probe_steps`` also keep
+                        the top-64 and the 256-index probe.  K/V slices after the
+                        prompt (layers 0/15/29 at four positions, every layer at the
+                        last prompt position).
+* ``teacher_config1.npz`` / ``teacher_ctx8192.npz``  teacher forcing: after the
+                        config-1 (ctx-8192) prompt, a seeded token sequence that
+                        changes at every step is fed one token at a time; per-step
+                        probes, full logits at the first and last steps and around
+                        the middle, and every layer's K/V rows at the fed positions.
+* ``permuted.npz``      free-running greedy stream of the untied permuted-head model
+                        (``synthetic.PERMUTED_HEAD_SPEC``), whose token changes at
+                        every step: 64 tokens with per-step probes and full logits
+                        at the first, second and last steps.
 * ``small128.npz``      the reference system test's geometry with vocab 128 and
-                        ids ``(arange*11+3) % 128`` (``tests/test_system.py:318-353``).
+                        ids ``(arange*11+3) % 128`` (``tests/test_system.py:318-353``),
+                        with the full logits of every step and every layer's K/V
+                        at the last prompt position.
 * ``ops.npz``           HF ``apply_rotary_pos_emb`` and ``LlamaRMSNorm`` input/output.
 * ``rope.npz``          HF ``rotary_emb`` cos/sin rows at selected positions.
 
-Run from the repo root: ``python tests/golden/make_golden.py``.
+Run from the repo root: ``python tests/golden/make_golden.py [name ...]`` (no
+names: every fixture).
 """
 
 from __future__ import annotations
@@ -54,8 +71,18 @@ def step_probes(logits: torch.Tensor, top: int = 64) -> dict[str, np.ndarray]:
     }
 
 
-def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int):
-    """Greedy decode with HF, recording per-step probes and K/V slices after the prompt."""
+def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int, *, probe_steps=None, teacher=None,
+                       full_logit_steps=(), kv_steps=()):
+    """Greedy (or teacher-forced) decode with HF, recording per-step probes and K/V slices.
+
+    Step 0's logits come from the prompt; step s >= 1 feeds ``teacher[s-1]`` when a
+    teacher sequence is given, else the previous step's argmax.  ``probe_steps``
+    (default: every step) get the top-64 and 256-index probe; every step gets the
+    token, the margin and the top-8.  ``full_logit_steps`` keep the whole logit
+    row; ``kv_steps`` keep every layer's K/V row written by that step's token.
+    """
+    steps = new_tokens if teacher is None else len(teacher) + 1
+    probe_steps = list(range(steps)) if probe_steps is None else [s for s in probe_steps if s < steps]
     with torch.inference_mode():
         out = model(input_ids=prompt, use_cache=True, logits_to_keep=1)
         cache = out.past_key_values
@@ -66,26 +93,53 @@ def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int):
             if layer < len(cache.layers):
                 kv[f"k{layer}"] = cache.layers[layer].keys[0][:, positions].numpy().copy()
                 kv[f"v{layer}"] = cache.layers[layer].values[0][:, positions].numpy().copy()
+        kv["k_all_last"] = np.stack([layer.keys[0][:, length - 1].numpy() for layer in cache.layers])
+        kv["v_all_last"] = np.stack([layer.values[0][:, length - 1].numpy() for layer in cache.layers])
         logits = out.logits[0, -1]
-        tokens, probes = [], []
-        for step in range(new_tokens):
-            probes.append(step_probes(logits))
+        tokens, probes, top8v, top8i, margins, full, kv_rows = [], [], [], [], [], [], []
+        for step in range(steps):
+            values, indices = torch.topk(logits.float(), 8)
+            top8v.append(values.numpy().astype(np.float32))
+            top8i.append(indices.numpy().astype(np.int64))
+            margins.append(np.float32(values[0] - values[1]))
+            if step in probe_steps:
+                probes.append(step_probes(logits))
+            if step in full_logit_steps:
+                full.append(logits.numpy().astype(np.float32).copy())
             token = int(torch.argmax(logits))
             tokens.append(token)
-            if step + 1 == new_tokens:
+            if step + 1 == steps:
                 break
-            out = model(input_ids=torch.tensor([[token]]), past_key_values=cache, use_cache=True,
+            fed = token if teacher is None else int(teacher[step])
+            out = model(input_ids=torch.tensor([[fed]]), past_key_values=cache, use_cache=True,
                         logits_to_keep=1)
             cache = out.past_key_values
             logits = out.logits[0, -1]
+            if step + 1 in kv_steps:
+                pos = length + step
+                kv_rows.append((np.stack([layer.keys[0][:, pos].numpy() for layer in cache.layers]),
+                                np.stack([layer.values[0][:, pos].numpy() for layer in cache.layers])))
     record = {
         "prompt": prompt[0].numpy().astype(np.int64),
         "tokens": np.asarray(tokens, dtype=np.int64),
         "kv_positions": np.asarray(positions, dtype=np.int64),
         "probe_indices": PROBE,
+        "probe_steps": np.asarray(probe_steps, dtype=np.int64),
+        "margin": np.asarray(margins, dtype=np.float32),
+        "top8_values": np.stack(top8v),
+        "top8_indices": np.stack(top8i),
     }
-    for key in ("top_values", "top_indices", "probe", "margin"):
+    for key in ("top_values", "top_indices", "probe"):
         record[key] = np.stack([p[key] for p in probes])
+    if teacher is not None:
+        record["teacher"] = np.asarray(teacher, dtype=np.int64)
+    if full_logit_steps:
+        record["full_logit_steps"] = np.asarray([s for s in full_logit_steps if s < steps], dtype=np.int64)
+        record["full_logits"] = np.stack(full)
+    if kv_steps:
+        record["kv_steps"] = np.asarray([s for s in kv_steps if s < steps], dtype=np.int64)
+        record["kv_step_k"] = np.stack([k for k, _ in kv_rows])
+        record["kv_step_v"] = np.stack([v for _, v in kv_rows])
     record.update(kv)
     return record
 
@@ -137,46 +191,108 @@ def ops_fixture(model) -> dict[str, np.ndarray]:
     }
 
 
-def main() -> None:
+def teacher_tokens(seed: int, count: int, vocab: int = 49152) -> np.ndarray:
+    """A seeded uniform token sequence with no two equal neighbours."""
+    rng = np.random.Generator(np.random.PCG64(5_000_011 + seed))
+    tokens = rng.integers(0, vocab, size=count, dtype=np.int64)
+    for i in range(1, count):
+        if tokens[i] == tokens[i - 1]:
+            tokens[i] = (tokens[i] + 1) % vocab
+    return tokens
+
+
+CONTEXT_LENGTHS = (128, 512, 1024, 2048, 4096, 8192)
+CONFIG2_STEPS = 128
+CONFIG5_STEPS = 513  # 8192-token prompt + 512 decode steps: positions 8192..8703
+
+
+def main(selected: set[str]) -> None:
     torch.set_num_threads(os.cpu_count() or 1)
-    meta: dict[str, object] = {"transformers": __import__("transformers").__version__,
-                               "torch": torch.__version__, "numpy": np.__version__}
+    want = (lambda name: not selected or name in selected)
+    meta_path = os.path.join(OUT, "weights.json")
+    meta: dict[str, object] = {}
+    if os.path.exists(meta_path):
+        with open(meta_path) as handle:
+            meta = json.load(handle)
+    meta.update({"transformers": __import__("transformers").__version__, "torch": torch.__version__,
+                 "numpy": np.__version__})
 
     spec = synthetic.SyntheticSpec(seed=0)
     model = synthetic.build_hf_model(spec)
     meta["weights_seed0_vocab49152"] = synthetic.weights_sha256(synthetic.synthetic_state_dict(spec))
-    np.savez_compressed(os.path.join(OUT, "rope.npz"), **rope_fixture(model))
-    np.savez_compressed(os.path.join(OUT, "ops.npz"), **ops_fixture(model))
+    if want("rope"):
+        np.savez_compressed(os.path.join(OUT, "rope.npz"), **rope_fixture(model))
+    if want("ops"):
+        np.savez_compressed(os.path.join(OUT, "ops.npz"), **ops_fixture(model))
 
-    t = time.time()
-    prompt = synthetic.synthetic_prompt(1, 128)
-    record = greedy_with_probes(model, prompt, 32)
-    check_against_generate(model, prompt, record["tokens"])
-    np.savez_compressed(os.path.join(OUT, "config1.npz"), **record)
-    print(f"config1 done in {time.time() - t:.1f}s tokens={record['tokens'][:8]}", flush=True)
-
-    for length, steps in ((512, 8), (1024, 8), (2048, 8), (8192, 4)):
+    if want("config1"):
         t = time.time()
+        prompt = synthetic.synthetic_prompt(1, 128)
+        record = greedy_with_probes(model, prompt, 32)
+        check_against_generate(model, prompt, record["tokens"])
+        np.savez_compressed(os.path.join(OUT, "config1.npz"), **record)
+        print(f"config1 done in {time.time() - t:.1f}s tokens={record['tokens'][:8]}", flush=True)
+
+    if want("teacher_config1"):
+        t = time.time()
+        prompt = synthetic.synthetic_prompt(1, 128)
+        teacher = teacher_tokens(1, 48)
+        record = greedy_with_probes(model, prompt, 0, teacher=teacher, full_logit_steps=(0, 1, 24, 48),
+                                    kv_steps=(1, 2, 24, 48))
+        np.savez_compressed(os.path.join(OUT, "teacher_config1.npz"), **record)
+        print(f"teacher_config1 done in {time.time() - t:.1f}s argmax={record['tokens'][:8]}", flush=True)
+
+    for length in CONTEXT_LENGTHS:
+        name = f"ctx{length}"
+        if not want(name) and not (length == 8192 and want("teacher_ctx8192")):
+            continue
         prompt = synthetic.synthetic_prompt(2, length)
-        record = greedy_with_probes(model, prompt, steps)
-        np.savez_compressed(os.path.join(OUT, f"ctx{length}.npz"), **record)
-        print(f"ctx{length} done in {time.time() - t:.1f}s margins={record['margin']}", flush=True)
+        if want(name):
+            t = time.time()
+            steps = CONFIG5_STEPS if length == 8192 else CONFIG2_STEPS
+            probe_steps = (0, 1, 2, 3, 31, 63, 127) + ((255, 511, 512) if length == 8192 else ())
+            record = greedy_with_probes(model, prompt, steps, probe_steps=probe_steps)
+            np.savez_compressed(os.path.join(OUT, f"{name}.npz"), **record)
+            print(f"{name} done in {time.time() - t:.1f}s tokens={sorted(set(record['tokens'].tolist()))} "
+                  f"min margin={record['margin'].min():.4f}", flush=True)
+        if length == 8192 and want("teacher_ctx8192"):
+            t = time.time()
+            teacher = teacher_tokens(2, 32)
+            record = greedy_with_probes(model, prompt, 0, teacher=teacher, full_logit_steps=(0, 1, 32),
+                                        kv_steps=(1, 32))
+            np.savez_compressed(os.path.join(OUT, "teacher_ctx8192.npz"), **record)
+            print(f"teacher_ctx8192 done in {time.time() - t:.1f}s", flush=True)
 
-    small = synthetic.SyntheticSpec(seed=2701, vocab=128)
-    small_model = synthetic.build_hf_model(small)
-    meta["weights_seed2701_vocab128"] = synthetic.weights_sha256(synthetic.synthetic_state_dict(small))
-    prompt = (torch.arange(7).unsqueeze(0) * 11 + 3) % 128
-    record = greedy_with_probes(small_model, prompt, 8)
-    check_against_generate(small_model, prompt, record["tokens"])
-    prompt17 = (torch.arange(17).unsqueeze(0) * 11 + 3) % 128
-    record17 = greedy_with_probes(small_model, prompt17, 4)
-    record.update({f"p17_{k}": v for k, v in record17.items()})
-    np.savez_compressed(os.path.join(OUT, "small128.npz"), **record)
+    if want("permuted"):
+        t = time.time()
+        pspec = synthetic.PERMUTED_HEAD_SPEC
+        pmodel = synthetic.build_hf_model(pspec)
+        meta["weights_permuted_head"] = synthetic.weights_sha256(synthetic.synthetic_state_dict(pspec))
+        prompt = synthetic.synthetic_prompt(1, 128)
+        record = greedy_with_probes(pmodel, prompt, 64, full_logit_steps=(0, 1, 63))
+        check_against_generate(pmodel, prompt, record["tokens"])
+        tokens = record["tokens"].tolist()
+        assert all(a != b for a, b in zip(tokens, tokens[1:])), "permuted-head stream repeats a token"
+        np.savez_compressed(os.path.join(OUT, "permuted.npz"), **record)
+        print(f"permuted done in {time.time() - t:.1f}s tokens={tokens[:8]} min margin={record['margin'].min():.3f}",
+              flush=True)
 
-    with open(os.path.join(OUT, "weights.json"), "w") as handle:
+    if want("small128"):
+        small = synthetic.SyntheticSpec(seed=2701, vocab=128)
+        small_model = synthetic.build_hf_model(small)
+        meta["weights_seed2701_vocab128"] = synthetic.weights_sha256(synthetic.synthetic_state_dict(small))
+        prompt = (torch.arange(7).unsqueeze(0) * 11 + 3) % 128
+        record = greedy_with_probes(small_model, prompt, 8, full_logit_steps=tuple(range(8)))
+        check_against_generate(small_model, prompt, record["tokens"])
+        prompt17 = (torch.arange(17).unsqueeze(0) * 11 + 3) % 128
+        record17 = greedy_with_probes(small_model, prompt17, 4, full_logit_steps=tuple(range(4)))
+        record.update({f"p17_{k}": v for k, v in record17.items()})
+        np.savez_compressed(os.path.join(OUT, "small128.npz"), **record)
+
+    with open(meta_path, "w") as handle:
         json.dump(meta, handle, indent=2, sort_keys=True)
     print("golden vectors written", flush=True)
 
 
 if __name__ == "__main__":
-    main()
+    main(set(sys.argv[1:]))

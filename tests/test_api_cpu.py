@@ -164,3 +164,44 @@ def test_audit_argument_validation():
 
     with pytest.raises(ValueError, match="audit capacity must exceed audit replays plus three warmups"):
         runtime_audit(_model(), capacity=10, replays=7)
+
+
+def _smol_geometry_model(vocab: int = 64) -> LlamaForCausalLM:
+    """SmolLM2 geometry (30 layers) on the meta device is too large to build per test on the CPU;
+    two of its layers suffice for the per-tensor checks, which iterate over model.model.layers."""
+    config = LlamaConfig(hidden_size=576, intermediate_size=1536, num_hidden_layers=2, num_attention_heads=9,
+                         num_key_value_heads=3, head_dim=64, vocab_size=vocab, max_position_embeddings=64,
+                         rms_norm_eps=1e-5, attention_bias=False, attention_dropout=0.0, mlp_bias=False,
+                         tie_word_embeddings=True)
+    config._attn_implementation = "eager"
+    torch.manual_seed(7)
+    model = LlamaForCausalLM(config).float().eval()
+    return smollm2_flux.enable_flux_ops(model, operators=smollm2_flux.FINAL_FLUX_OPERATOR_CATEGORIES)
+
+
+def test_weight_tensors_are_checked_before_the_native_boundary():
+    """Every weight pointer handed to the C ABI comes from a tensor checked for device, dtype,
+    shape and contiguity (the kernels read raw pointers; a strided, host-resident or wrong-shape
+    weight must be refused with a clean error, not read)."""
+    from flux_amd.runtime.native_smollm2 import _model_weight_tensors
+
+    model = _smol_geometry_model()
+    cpu = torch.device("cpu")
+    tensors = _model_weight_tensors(model, cpu)
+    assert len(tensors) == 3 + 6 * 2
+    assert tensors[0].data_ptr() == tensors[1].data_ptr()  # tied LM head
+    with pytest.raises(ValueError, match="embedding weight is on cpu, expected cuda:0"):
+        _model_weight_tensors(model, torch.device("cuda", 0))
+    layer = model.model.layers[1]
+    original = layer.self_attn.o_proj.weight
+    layer.self_attn.o_proj.weight = torch.nn.Parameter(original.detach().t().contiguous().t())
+    assert not layer.self_attn.o_proj.weight.is_contiguous()
+    with pytest.raises(ValueError, match="layer 1 o_proj weight must be contiguous"):
+        _model_weight_tensors(model, cpu)
+    layer.self_attn.o_proj.weight = original
+    layer.mlp.down_proj.weight = torch.nn.Parameter(torch.zeros(576, 1535))
+    with pytest.raises(ValueError, match=r"layer 1 down weight has shape \[576, 1535\], expected \[576, 1536\]"):
+        _model_weight_tensors(model, cpu)
+    layer.mlp.down_proj.weight = torch.nn.Parameter(torch.zeros(576, 1536, dtype=torch.float64))
+    with pytest.raises(ValueError, match="layer 1 down weight has dtype torch.float64"):
+        _model_weight_tensors(model, cpu)

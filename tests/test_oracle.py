@@ -88,6 +88,123 @@ def test_oracle_matches_hf_config1(smol_oracle):
         torch.testing.assert_close(k, torch.from_numpy(record[f"k{layer}"]), rtol=1e-5, atol=1e-6)
 
 
+def _full_check(logits: torch.Tensor, record: dict, step: int, atol: float = 1e-5) -> None:
+    """Top-8 at every step, top-64 + probe at the probe steps, every logit at the full-logit steps."""
+    torch.testing.assert_close(logits[torch.from_numpy(record["top8_indices"][step])],
+                               torch.from_numpy(record["top8_values"][step]), atol=atol, rtol=1e-5)
+    steps = record["probe_steps"].tolist()
+    if step in steps:
+        _probe_check(logits, record, steps.index(step), atol)
+    if "full_logit_steps" in record and step in record["full_logit_steps"].tolist():
+        i = record["full_logit_steps"].tolist().index(step)
+        torch.testing.assert_close(logits, torch.from_numpy(record["full_logits"][i]), atol=atol, rtol=1e-5)
+
+
+def test_oracle_matches_hf_teacher_forced_stream(smol_oracle):
+    """A token sequence that changes at every step, fed after the config-1 prompt: all 49 steps
+    agree with HF (every logit at steps 0, 1, 24, 48) and so do the K/V rows the fed tokens write."""
+    record = golden("teacher_config1.npz")
+    teacher = record["teacher"].tolist()
+    assert len(teacher) == 48 and all(a != b for a, b in zip(teacher, teacher[1:]))
+    cache = OracleCache()
+    prompt_len = len(record["prompt"])
+    kv_steps = record["kv_steps"].tolist()
+    with torch.inference_mode():
+        logits = smol_oracle.forward(torch.from_numpy(record["prompt"]).unsqueeze(0), cache)[0, -1]
+        _full_check(logits, record, 0)
+        for step in range(1, len(teacher) + 1):
+            logits = smol_oracle.forward(torch.tensor([[teacher[step - 1]]]), cache)[0, -1]
+            _full_check(logits, record, step)
+            assert int(torch.argmax(logits)) == int(record["tokens"][step])
+            if step in kv_steps:
+                pos = prompt_len + step - 1
+                k = torch.stack([cache.keys[layer][0, :, pos] for layer in range(30)])
+                torch.testing.assert_close(k, torch.from_numpy(record["kv_step_k"][kv_steps.index(step)]),
+                                           rtol=1e-5, atol=1e-6)
+
+
+def test_oracle_matches_hf_permuted_head_stream():
+    """The untied permuted-head model's greedy stream changes at every step (its successor rule is
+    argsort(perm)[token] when the scaled embedding dominates); the oracle reproduces HF's 64 tokens."""
+    spec = synthetic.PERMUTED_HEAD_SPEC
+    state = synthetic.synthetic_state_dict(spec)
+    with open(os.path.join(GOLDEN, "weights.json")) as handle:
+        assert synthetic.weights_sha256(state) == json.load(handle)["weights_permuted_head"]
+    assert state["lm_head.weight"] is not state["model.embed_tokens.weight"]
+    record = golden("permuted.npz")
+    tokens, logits, _ = OracleLlama(state).greedy(torch.from_numpy(record["prompt"]).unsqueeze(0),
+                                                  len(record["tokens"]), keep_logits=True)
+    assert tokens == record["tokens"].tolist()
+    for step, row in enumerate(logits):
+        _full_check(row, record, step, atol=2e-5)
+    perm = np.random.Generator(np.random.PCG64(spec.permuted_head_seed)).permutation(spec.vocab)
+    successor = np.argsort(perm)
+    assert sum(int(successor[a]) == b for a, b in zip(tokens, tokens[1:])) >= 48
+
+
+def test_oracle_matches_hf_context_streams(smol_oracle):
+    """Config-2 prompts of 128 and 512 tokens: the first 16 greedy steps agree with HF."""
+    for length in (128, 512):
+        record = golden(f"ctx{length}.npz")
+        assert len(record["tokens"]) == 128
+        prompt = torch.from_numpy(record["prompt"]).unsqueeze(0)
+        assert torch.equal(prompt, synthetic.synthetic_prompt(2, length))
+        tokens, logits, cache = smol_oracle.greedy(prompt, 16, keep_logits=True)
+        assert tokens == record["tokens"][:16].tolist()
+        for step, row in enumerate(logits):
+            _full_check(row, record, step)
+        last = torch.stack([cache.keys[layer][0, :, length - 1] for layer in range(30)])
+        torch.testing.assert_close(last, torch.from_numpy(record["k_all_last"]), rtol=1e-5, atol=1e-6)
+
+
+def test_qkv_rope_cache_pinned_to_hf_layer0():
+    """oracle.kernels.qkv_rope_cache against HF: layer 0 of the config-1 prompt (embedding rows,
+    unit norm, packed q/k/v rows, the position's RoPE row) gives HF's cached K and V rows; and its
+    q/k agree with rope_rows (HF apply_rotary_pos_emb rounding) applied to the GEMV output."""
+    record = golden("config1.npz")
+    state = synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=0))
+    emb = state["model.embed_tokens.weight"]
+    p = "model.layers.0."
+    packed = torch.cat([state[p + "self_attn.q_proj.weight"], state[p + "self_attn.k_proj.weight"],
+                        state[p + "self_attn.v_proj.weight"]])
+    norm_w = state[p + "input_layernorm.weight"]
+    positions = record["kv_positions"].tolist()
+    cos, sin = rope_table(OracleConfig(), max(positions) + 1)
+    for i, pos in enumerate(positions):
+        hidden = emb[int(record["prompt"][pos])]
+        q, k, v = ref.qkv_rope_cache(hidden, norm_w, 1e-5, packed, cos[pos], sin[pos])
+        torch.testing.assert_close(k.float(), torch.from_numpy(record["k0"][:, i]), rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(v.float(), torch.from_numpy(record["v0"][:, i]), rtol=1e-5, atol=1e-6)
+        qkv = packed.double() @ ref.rmsnorm(hidden, norm_w, 1e-5)
+        torch.testing.assert_close(q.float(), ref.rope_rows(qkv[:576].float().view(9, 64), cos[pos], sin[pos]),
+                                   rtol=1e-5, atol=1e-6)
+    # A RoPE with the rotation sign flipped, or q/k routed from the wrong rows, misses HF's K row.
+    pos = positions[-1]
+    hidden = emb[int(record["prompt"][pos])]
+    _, k, _ = ref.qkv_rope_cache(hidden, norm_w, 1e-5, packed, cos[pos], -sin[pos])
+    assert not torch.allclose(k.float(), torch.from_numpy(record["k0"][:, -1]), rtol=1e-5, atol=1e-6)
+    _, k2, _ = ref.qkv_rope_cache(hidden, norm_w, 1e-5, packed[[*range(576, 768), *range(576), *range(768, 960)]],
+                                  cos[pos], sin[pos])
+    assert not torch.allclose(k2.float(), torch.from_numpy(record["k0"][:, -1]), rtol=1e-5, atol=1e-6)
+
+
+def test_product_rope_tables_match_hf():
+    """The runtime's host RoPE tables (native_smollm2._rope_tables, built from the model's own
+    inv_freq) are bit-identical to transformers' rotary_emb output at 8704 positions."""
+    from types import SimpleNamespace
+
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    from flux_amd.runtime.native_smollm2 import _rope_tables
+
+    record = golden("rope.npz")
+    rotary = LlamaRotaryEmbedding(synthetic.llama_config())
+    cos, sin = _rope_tables(SimpleNamespace(model=SimpleNamespace(rotary_emb=rotary)), 8704)
+    assert cos.shape == sin.shape == (8704, 64) and cos.dtype == torch.float32
+    assert hashlib.sha256(cos.numpy().tobytes()).digest() == record["cos_sha256"].tobytes()
+    assert hashlib.sha256(sin.numpy().tobytes()).digest() == record["sin_sha256"].tobytes()
+
+
 def test_rope_table_matches_hf_rotary_embedding():
     record = golden("rope.npz")
     cos, sin = rope_table(OracleConfig(), 8704)

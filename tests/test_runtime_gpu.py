@@ -4,6 +4,12 @@ Mirrors the reference system tests (tests/test_system.py:356-497): logits and
 K/V caches against the HF path, exact greedy token equality, position/length/
 step invariants, capacity exhaustion, prefill reuse and reset.  Golden vectors
 were written by tests/golden/make_golden.py from transformers on the CPU.
+
+The token loop is pinned with streams whose token changes at every step:
+teacher forcing through ``replay(token)`` with a seeded token sequence
+(``teacher_*.npz``), and the free-running greedy stream of the untied
+permuted-head model (``permuted.npz``), whose successor token differs at every
+step, so the on-device argmax feedback is what decides each step's input.
 """
 
 from __future__ import annotations
@@ -27,19 +33,33 @@ KV_RTOL = 2e-4
 KV_ATOL = 2e-5
 
 
-def _check_probes(logits: torch.Tensor, record: dict, step: int) -> None:
-    """Compare a [vocab] logit vector with the golden top-64 and probe slices of `step`."""
+def _assert_logits(values: torch.Tensor, expected: np.ndarray | torch.Tensor) -> None:
+    expected = torch.as_tensor(expected, dtype=torch.float32)
+    torch.testing.assert_close(values, expected, atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
+
+
+def _check_step(logits: torch.Tensor, record: dict, step: int) -> None:
+    """Compare a [vocab] logit row with the golden vectors of `step`.
+
+    Every step: the top-8 logits.  Probe steps: the top-64 and the 256-index probe.
+    Full-logit steps: all logits."""
     values = logits.detach().float().cpu()
-    top_idx = torch.from_numpy(record["top_indices"][step])
-    torch.testing.assert_close(values[top_idx], torch.from_numpy(record["top_values"][step]),
-                               atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
-    probe_idx = torch.from_numpy(record["probe_indices"])
-    probe_idx = probe_idx[probe_idx < values.numel()]
-    torch.testing.assert_close(values[probe_idx], torch.from_numpy(record["probe"][step]),
-                               atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
+    if "top8_indices" in record:
+        _assert_logits(values[torch.from_numpy(record["top8_indices"][step])], record["top8_values"][step])
+    steps = record["probe_steps"].tolist() if "probe_steps" in record else list(range(len(record["top_values"])))
+    if step in steps:
+        i = steps.index(step)
+        _assert_logits(values[torch.from_numpy(record["top_indices"][i])], record["top_values"][i])
+        probe_idx = torch.from_numpy(record["probe_indices"])
+        probe_idx = probe_idx[probe_idx < values.numel()]
+        _assert_logits(values[probe_idx], record["probe"][i])
+    if "full_logit_steps" in record and step in record["full_logit_steps"].tolist():
+        i = record["full_logit_steps"].tolist().index(step)
+        _assert_logits(values, record["full_logits"][i])
 
 
 def _check_kv(runtime, record: dict) -> None:
+    """K/V slices after the prompt: layers 0/15/29 at four positions, every layer at the last."""
     positions = torch.from_numpy(record["kv_positions"])
     for layer in (0, 15, 29):
         if f"k{layer}" not in record:
@@ -48,30 +68,79 @@ def _check_kv(runtime, record: dict) -> None:
         v = runtime.value_cache[layer, 0][:, positions].float().cpu()
         torch.testing.assert_close(k, torch.from_numpy(record[f"k{layer}"]), rtol=KV_RTOL, atol=KV_ATOL)
         torch.testing.assert_close(v, torch.from_numpy(record[f"v{layer}"]), rtol=KV_RTOL, atol=KV_ATOL)
+    if "k_all_last" in record:
+        last = len(record["prompt"]) - 1
+        torch.testing.assert_close(runtime.key_cache[:, 0, :, last].float().cpu(),
+                                   torch.from_numpy(record["k_all_last"]), rtol=KV_RTOL, atol=KV_ATOL)
+        torch.testing.assert_close(runtime.value_cache[:, 0, :, last].float().cpu(),
+                                   torch.from_numpy(record["v_all_last"]), rtol=KV_RTOL, atol=KV_ATOL)
 
 
-def _teacher_forced(runtime, record: dict) -> None:
-    """Step 0 from prefill logits, then replay the golden tokens one by one."""
-    tokens = record["tokens"]
-    _check_probes(runtime.logits[0, 0], record, 0)
-    for step in range(1, len(tokens)):
-        token = torch.tensor([[int(tokens[step - 1])]], dtype=torch.long, device=runtime.logits.device)
+def _replay_stream(runtime, record: dict, fed: list[int], steps: int) -> None:
+    """Step 0 from the prefill logits, then replay fed[s-1] for s = 1 .. steps-1, checking each step.
+
+    Where the record keeps every layer's K/V row of a step (``kv_steps``), the row
+    written at that step's position is checked too."""
+    device = runtime.logits.device
+    prompt_len = len(record["prompt"])
+    kv_steps = record["kv_steps"].tolist() if "kv_steps" in record else []
+    _check_step(runtime.logits[0, 0], record, 0)
+    for step in range(1, steps):
+        token = torch.tensor([[int(fed[step - 1])]], dtype=torch.long, device=device)
         logits = runtime.replay(token)
         torch.cuda.synchronize()
-        _check_probes(logits[0, 0], record, step)
+        _check_step(logits[0, 0], record, step)
+        if step in kv_steps:
+            i = kv_steps.index(step)
+            pos = prompt_len + step - 1
+            torch.testing.assert_close(runtime.key_cache[:, 0, :, pos].float().cpu(),
+                                       torch.from_numpy(record["kv_step_k"][i]), rtol=KV_RTOL, atol=KV_ATOL)
+            torch.testing.assert_close(runtime.value_cache[:, 0, :, pos].float().cpu(),
+                                       torch.from_numpy(record["kv_step_v"][i]), rtol=KV_RTOL, atol=KV_ATOL)
+    assert runtime.cache_position == prompt_len + steps - 1
+
+
+def _decode_logits(runtime: NativeSmolLM2Prefill) -> torch.Tensor:
+    """The decode runtime's logits row (the last decode step's; ``runtime.logits`` is the
+    prefill's, as in the reference, native_prefill_runtime_cuda.cu:748)."""
+    return runtime.native_object().decode.logits[0, 0]
+
+
+def _capture(model, record: dict, decode_steps: int) -> NativeSmolLM2Prefill:
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
+    runtime = NativeSmolLM2Prefill.capture(model, prompt, max_decode_steps=decode_steps)
+    torch.cuda.synchronize()
+    return runtime
+
+
+@pytest.fixture(scope="module")
+def permuted_model(gpu_device):
+    from flux_amd.model import FINAL_FLUX_OPERATOR_CATEGORIES, enable_flux_ops
+
+    model = synthetic.build_hf_model(synthetic.PERMUTED_HEAD_SPEC, device=gpu_device)
+    enable_flux_ops(model, operators=FINAL_FLUX_OPERATOR_CATEGORIES)
+    return model
 
 
 def test_small_vocab_prefill_decode_matches_hf(small_model):
+    """Vocab-128 model: every step's full logits against HF, every layer's whole K/V cache against the oracle."""
     record = golden("small128.npz")
     prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
     tokens = record["tokens"]
-    runtime = NativeSmolLM2Prefill.capture(small_model, prompt, max_decode_steps=len(tokens) - 1)
-    torch.cuda.synchronize()
+    runtime = _capture(small_model, record, len(tokens) - 1)
     assert runtime.prompt_length == runtime.cache_position == runtime.cache_length == prompt.shape[1]
     assert runtime.key_cache.shape == (30, 1, 3, prompt.shape[1] + len(tokens) - 1, 64)
     _check_kv(runtime, record)
-    _teacher_forced(runtime, record)
+    _replay_stream(runtime, record, tokens.tolist(), len(tokens))
     assert runtime.cache_position == runtime.cache_length == prompt.shape[1] + len(tokens) - 1
+    # Every layer, every position: the oracle's cache after the same token stream.
+    oracle = OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128)))
+    _, _, cache = oracle.greedy(prompt.cpu(), len(tokens))
+    for layer in range(30):
+        torch.testing.assert_close(runtime.key_cache[layer].float().cpu(), cache.keys[layer], rtol=KV_RTOL,
+                                   atol=KV_ATOL)
+        torch.testing.assert_close(runtime.value_cache[layer].float().cpu(), cache.values[layer], rtol=KV_RTOL,
+                                   atol=KV_ATOL)
     with pytest.raises(RuntimeError, match="exhausted"):
         runtime.replay(torch.tensor([[int(tokens[-1])]], device="cuda"))
     assert runtime.device_error() == 0
@@ -89,6 +158,7 @@ def test_small_vocab_greedy_generation_exact(small_model):
     assert generated.shape == (1, n)
     assert generated[0].cpu().equal(expected)
     assert generated[:, :1].equal(runtime.prefill_logits.argmax(dim=-1))
+    _assert_logits(_decode_logits(runtime).cpu(), record["full_logits"][n - 1])
     assert runtime.cache_position == runtime.cache_length == prompt.shape[1] + n - 1
     assert runtime.generation_step == n
     assert runtime.stable_addresses() == addresses
@@ -109,33 +179,120 @@ def test_small_vocab_greedy_generation_exact(small_model):
 def test_config1_tokens_and_logits(smol_model):
     """Config 1: 128-token prompt, 32 greedy tokens (golden from HF eager FP32)."""
     record = golden("config1.npz")
-    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
     n = len(record["tokens"])
-    runtime = NativeSmolLM2Prefill.capture(smol_model, prompt, max_decode_steps=n - 1)
-    torch.cuda.synchronize()
+    runtime = _capture(smol_model, record, n - 1)
     _check_kv(runtime, record)
-    _teacher_forced(runtime, record)
-    runtime.prefill(prompt)
+    _replay_stream(runtime, record, record["tokens"].tolist(), n)
+    runtime.prefill(torch.from_numpy(record["prompt"]).unsqueeze(0).cuda())
     generated = runtime.generate_greedy(n).clone()
     torch.cuda.synchronize()
     assert generated[0].cpu().numpy().tolist() == record["tokens"].tolist()
     assert runtime.device_error() == 0
 
 
-@pytest.mark.parametrize("length", [512, 1024, 2048, 8192])
-def test_context_prefill_decode_matches_hf(smol_model, length):
-    """Config 2/3 prompts: prefill caches + logits and greedy tokens vs golden."""
-    record = golden(f"ctx{length}.npz")
-    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
-    n = len(record["tokens"])
-    runtime = NativeSmolLM2Prefill.capture(smol_model, prompt, max_decode_steps=n - 1)
-    torch.cuda.synchronize()
+@pytest.mark.parametrize("name", ["teacher_config1", "teacher_ctx8192"])
+def test_teacher_forced_changing_tokens(smol_model, name):
+    """replay(token) with a seeded token sequence that changes at every step (48 steps after the
+    config-1 prompt, 32 after the 8192-token prompt): per-step probes, all 49152 logits at the first,
+    middle and last steps, and every layer's K/V row written at the fed positions."""
+    record = golden(f"{name}.npz")
+    teacher = record["teacher"].tolist()
+    assert all(a != b for a, b in zip(teacher, teacher[1:]))
+    runtime = _capture(smol_model, record, len(teacher))
     _check_kv(runtime, record)
-    _teacher_forced(runtime, record)
-    runtime.prefill(prompt)
+    _replay_stream(runtime, record, teacher, len(teacher) + 1)
+    assert runtime.device_error() == 0
+
+
+def test_permuted_head_free_running_stream(permuted_model):
+    """Untied permuted-head model: the HF greedy stream changes at every step, so each decode
+    step's input is the previous step's on-device argmax.  64 tokens from one generate_greedy
+    call must equal HF's exactly; the step-by-step replay of the same stream checks the
+    logits of every step and all logits at steps 0, 1 and 63."""
+    record = golden("permuted.npz")
+    tokens = record["tokens"]
+    n = len(tokens)
+    assert all(a != b for a, b in zip(tokens.tolist(), tokens[1:].tolist()))
+    runtime = _capture(permuted_model, record, n - 1)
     generated = runtime.generate_greedy(n).clone()
     torch.cuda.synchronize()
-    assert generated[0].cpu().numpy().tolist() == record["tokens"].tolist()
+    assert generated[0].cpu().numpy().tolist() == tokens.tolist()
+    _assert_logits(_decode_logits(runtime).cpu(), record["full_logits"][-1])
+    assert runtime.device_error() == 0
+    runtime.prefill(torch.from_numpy(record["prompt"]).unsqueeze(0).cuda())
+    torch.cuda.synchronize()
+    _replay_stream(runtime, record, tokens.tolist(), n)
+
+
+@pytest.mark.parametrize("length", [128, 512, 1024, 2048, 4096, 8192])
+def test_config2_context_decode_matches_hf(smol_model, length):
+    """Config 2 (and config 3 prompts): prefill K/V and logits, then 128 decode steps both
+    teacher-forced through replay() (top-8 every step, top-64 + probe at steps 0-3/31/63/127)
+    and free-running in one generate_greedy call (tokens exact)."""
+    record = golden(f"ctx{length}.npz")
+    steps = 128
+    runtime = _capture(smol_model, record, steps - 1)
+    _check_kv(runtime, record)
+    _replay_stream(runtime, record, record["tokens"].tolist(), steps)
+    runtime.prefill(torch.from_numpy(record["prompt"]).unsqueeze(0).cuda())
+    generated = runtime.generate_greedy(steps).clone()
+    torch.cuda.synchronize()
+    assert generated[0].cpu().numpy().tolist() == record["tokens"][:steps].tolist()
+    _check_step(_decode_logits(runtime), record, steps - 1)
+    assert runtime.device_error() == 0
+
+
+def test_config5_8192_plus_512_steps(smol_model):
+    """Config 5: 8192-token prefill handed to 512 decode steps in one generate_greedy(513) call;
+    the last step writes position 8703 and the cache holds 8704 positions.  All 513 tokens match
+    HF, the final logits match HF's step-512 probes, and a second run is bitwise identical."""
+    record = golden("ctx8192.npz")
+    assert len(record["tokens"]) == 513
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
+    runtime = NativeSmolLM2Prefill.capture(smol_model, prompt, max_decode_steps=512)
+    assert runtime.capacity == 8704
+    first = runtime.generate_greedy(513).clone()
+    logits_first = _decode_logits(runtime).clone()
+    torch.cuda.synchronize()
+    assert first[0].cpu().numpy().tolist() == record["tokens"].tolist()
+    _check_step(logits_first, record, 512)
+    assert runtime.cache_position == runtime.cache_length == 8704
+    assert runtime.generation_step == 513
+    runtime.prefill(prompt)
+    second = runtime.generate_greedy(513).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+    assert torch.equal(logits_first, _decode_logits(runtime))
+    assert runtime.device_error() == 0
+
+
+def test_zero_weight_runtime_closed_form(gpu_device):
+    """Reference closed form (csrc/tests/test_native_runtimes.cu:32-78): with every linear and
+    embedding weight zero and unit norms, every logit is exactly 0 and every greedy token is 0
+    (lowest index of the maximum), through prefill, replay and generate_greedy."""
+    from flux_amd.model import FINAL_FLUX_OPERATOR_CATEGORIES, enable_flux_ops
+
+    model = synthetic.build_hf_model(synthetic.SyntheticSpec(seed=7, vocab=32), device=gpu_device)
+    with torch.no_grad():
+        for name, param in model.named_parameters():
+            if "norm" not in name:
+                param.zero_()
+    enable_flux_ops(model, operators=FINAL_FLUX_OPERATOR_CATEGORIES)
+    prompt = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6, 5, 3]], device=gpu_device)
+    runtime = NativeSmolLM2Prefill.capture(model, prompt, max_decode_steps=12)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(runtime.prefill_logits).item() == 0
+    assert int(runtime.current_token.item()) == 0
+    logits = runtime.replay(torch.tensor([[17]], device=gpu_device))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(logits).item() == 0
+    runtime.prefill(prompt)
+    generated = runtime.generate_greedy(13).clone()
+    torch.cuda.synchronize()
+    assert generated.cpu().tolist() == [[0] * 13]
+    assert torch.count_nonzero(_decode_logits(runtime)).item() == 0
+    assert torch.count_nonzero(runtime.key_cache).item() == 0
+    assert runtime.cache_position == 22
     assert runtime.device_error() == 0
 
 
@@ -170,28 +327,6 @@ def test_prefill_input_errors(small_model):
         native.prefill(ids[:, :-1])
 
 
-def test_end_to_end_8192_plus_512_is_deterministic(smol_model):
-    """Config 5 shape: 8192-token prefill handed to 512 greedy steps in one call.
-
-    Golden tokens exist for the first 4 steps; the full run must be bitwise
-    repeatable and keep the position/step invariants."""
-    record = golden("ctx8192.npz")
-    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
-    runtime = NativeSmolLM2Prefill.capture(smol_model, prompt, max_decode_steps=511)
-    first = runtime.generate_greedy(512).clone()
-    logits_first = runtime.logits.clone()
-    torch.cuda.synchronize()
-    assert first[0, :4].cpu().numpy().tolist() == record["tokens"].tolist()
-    assert runtime.cache_position == 8192 + 511
-    assert runtime.generation_step == 512
-    runtime.prefill(prompt)
-    second = runtime.generate_greedy(512).clone()
-    torch.cuda.synchronize()
-    assert torch.equal(first, second)
-    assert torch.equal(logits_first, runtime.logits)
-    assert runtime.device_error() == 0
-
-
 @pytest.mark.parametrize("length", [1, 45, 333, 1537, 3001])
 def test_odd_length_prefill_matches_oracle(small_model, length):
     """Prompt lengths that end inside a 128-query attention tile and split the keys of the
@@ -217,3 +352,33 @@ def test_odd_length_prefill_matches_oracle(small_model, length):
         v = runtime.value_cache[layer, 0][:, positions].float().cpu()
         torch.testing.assert_close(k, cache.keys[layer][0][:, positions], rtol=KV_RTOL, atol=KV_ATOL)
         torch.testing.assert_close(v, cache.values[layer][0][:, positions], rtol=KV_RTOL, atol=KV_ATOL)
+
+
+def test_wait_timeout_reports_error_and_invalid_tokens(small_model):
+    """Failure handling, forced from the host: a zero bound on the fused kernel's
+    cross-workgroup waits makes them give up at once (every kernel still exits normally).
+    The launch reports token -1 for every step, the next runtime call raises a device error
+    instead of returning plausible results, and prefill re-arms the runtime."""
+    record = golden("small128.npz")
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0).cuda()
+    n = len(record["tokens"])
+    runtime = NativeSmolLM2Prefill.capture(small_model, prompt, max_decode_steps=n - 1)
+    handle = runtime.native_object().decode
+    assert isinstance(handle.cooperative_graph(), bool)
+    first = runtime.generate_greedy(n).clone()
+    torch.cuda.synchronize()
+    assert first[0].cpu().numpy().tolist() == record["tokens"].tolist()
+    runtime.prefill(prompt)
+    handle.set_wait_limit(0)
+    failed = runtime.generate_greedy(n).clone()
+    torch.cuda.synchronize()
+    assert failed[0, 1:].cpu().tolist() == [-1] * (n - 1)  # slot 0 is the prefill's token
+    assert runtime.device_error() == 1
+    with pytest.raises(RuntimeError, match="device-side error 1"):
+        runtime.replay(torch.tensor([[int(record["tokens"][0])]], device="cuda"))
+    handle.set_wait_limit(20_000_000)
+    runtime.prefill(prompt)
+    again = runtime.generate_greedy(n).clone()
+    torch.cuda.synchronize()
+    assert again[0].cpu().numpy().tolist() == record["tokens"].tolist()
+    assert runtime.device_error() == 0
