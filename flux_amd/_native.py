@@ -158,6 +158,8 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_gqa_decode_workspace_bytes", ctypes.c_int, [ctypes.c_int64, _i64]),
     ("flux_gqa_decode_attention_f32", ctypes.c_int,
      [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_float, _vp, ctypes.c_int64, _vp, _stream]),
+    ("flux_gqa_decode_attention_noalloc_f32", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_float, _vp, _stream]),
     ("flux_linear576_f32", ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int64, _stream]),
     ("flux_gate_up_swiglu_f32", ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _vp, _stream]),
     ("flux_down_residual_f32", ctypes.c_int, [_vp, _vp, _vp, _vp, _stream]),

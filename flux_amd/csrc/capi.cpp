@@ -55,6 +55,7 @@ int from_hip(hipError_t status, const char* what) {
 }
 
 int invalid(const char* message) { return fail(FLUX_ERROR_INVALID_VALUE, message); }
+int invalid(const std::string& message) { return fail(FLUX_ERROR_INVALID_VALUE, message); }
 
 int isolated_grid() {
     int cus = 0;
@@ -272,6 +273,23 @@ int flux_gqa_decode_attention_f32(const float* q, const float* key_cache, const 
     return from_hip(flux::launch_gqa_decode(q, key_cache, value_cache, position, capacity, scale,
                                             isolated_chunks(capacity), static_cast<float*>(workspace), out, stream),
                     "flux_gqa_decode_attention_f32");
+}
+
+int flux_gqa_decode_attention_noalloc_f32(const float* q, const float* key_cache, const float* value_cache,
+                                          const int64_t* position, int64_t capacity, float scale, float* out,
+                                          hipStream_t stream) {
+    if (!q || !key_cache || !value_cache || !position || !out)
+        return invalid("flux_gqa_decode_attention_noalloc_f32: null argument");
+    if (capacity <= 0 || capacity > FLUX_MAX_CAPACITY)
+        return invalid("flux_gqa_decode_attention_noalloc_f32: capacity " + std::to_string(capacity) +
+                       " is outside [1, " + std::to_string(FLUX_MAX_CAPACITY) +
+                       "], the most positions its fixed scratch array holds partials for");
+    const int chunks = isolated_chunks(capacity);
+    if (chunks > flux::gqa_decode_noalloc_max_chunks())
+        return invalid("flux_gqa_decode_attention_noalloc_f32: capacity needs more partials than the scratch holds");
+    return from_hip(flux::launch_gqa_decode_noalloc(q, key_cache, value_cache, position, capacity, scale, chunks, out,
+                                                    stream),
+                    "flux_gqa_decode_attention_noalloc_f32");
 }
 
 int flux_linear576_f32(const float* x, const float* weight, const float* residual, float* out, int64_t rows,

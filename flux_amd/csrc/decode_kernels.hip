@@ -31,6 +31,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <mutex>
 
 namespace flux {
 namespace {
@@ -1363,6 +1364,42 @@ __global__ void install_state_kernel(const int64_t* token_src, int64_t position_
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Scratch of the allocation-free GQA decode entry point: the split-K partials of one
+// call, (chunks x 3 KV heads x 3 query heads x 66) floats for the 85 chunks that cover
+// every capacity up to FLUX_MAX_CAPACITY (85 x 224 = 19040 positions): 201,960 bytes.
+// Each GPU the library runs on holds its own copy until the process ends.  Every call
+// on one GPU shares it: calls that overlap on one GPU race.  Each call writes every
+// partial it later merges, so nothing needs clearing between calls.
+constexpr int kNoAllocChunks = 85;
+constexpr size_t kNoAllocScratchFloats = static_cast<size_t>(kNoAllocChunks) * kKVHeads * kGroup * (kHeadDim + 2);
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+// Host code must not pass `scratch` itself to a kernel (on the host it names a stand-in,
+// not the device copy): its device address is looked up once per device, with that
+// device current, and kept here.
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static float* g_scratch_address[kMaxScratchDevices] = {};
+
+static hipError_t scratch_address(float** out) {
+    int device = -1;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) return st;
+    if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_address[device] == nullptr) {
+        void* address = nullptr;
+        st = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (st != hipSuccess) return st;
+        g_scratch_address[device] = static_cast<float*>(address);
+    }
+    *out = g_scratch_address[device];
+    return hipSuccess;
+}
+
+int gqa_decode_noalloc_max_chunks() { return kNoAllocChunks; }
+
+// ---------------------------------------------------------------------------
 // Host launchers.
 
 size_t ll_arena_words() { return LLLayout::kTotal; }
@@ -1432,6 +1469,17 @@ hipError_t launch_gqa_decode(const float* q, const float* key_cache, const float
 }
 
 int gqa_decode_max_positions(int chunks) { return chunks * kAttnRows; }
+
+// The split-K partials go to this GPU's `scratch` copy; no allocation of any kind.
+hipError_t launch_gqa_decode_noalloc(const float* q, const float* key_cache, const float* value_cache,
+                                     const int64_t* position, int64_t capacity, float scale, int chunks, float* out,
+                                     hipStream_t stream) {
+    if (chunks < 1 || chunks > kNoAllocChunks) return hipErrorInvalidValue;
+    float* partials = nullptr;
+    hipError_t st = scratch_address(&partials);
+    if (st != hipSuccess) return st;
+    return launch_gqa_decode(q, key_cache, value_cache, position, capacity, scale, chunks, partials, out, stream);
+}
 
 hipError_t launch_linear576_residual(const float* x, const float* w, const float* residual, float* out, int rows,
                                      int grid, hipStream_t stream) {

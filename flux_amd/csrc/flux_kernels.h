@@ -56,6 +56,12 @@ hipError_t launch_gqa_decode(const float* q, const float* key_cache, const float
                              int64_t capacity, float scale, int chunks, float* partials, float* out,
                              hipStream_t stream);
 int gqa_decode_max_positions(int chunks);
+// launch_gqa_decode with the partials in the library's per-device scratch array
+// (chunks <= gqa_decode_noalloc_max_chunks()); allocates nothing.
+hipError_t launch_gqa_decode_noalloc(const float* q, const float* key_cache, const float* value_cache,
+                                     const int64_t* position, int64_t capacity, float scale, int chunks, float* out,
+                                     hipStream_t stream);
+int gqa_decode_noalloc_max_chunks();
 hipError_t launch_linear576_residual(const float* x, const float* w, const float* residual, float* out, int rows,
                                      int grid, hipStream_t stream);
 hipError_t launch_gate_up_swiglu(const float* hidden, const float* norm_w, float eps, const float* gate_up, float* out,

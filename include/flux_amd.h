@@ -291,6 +291,19 @@ int flux_gqa_decode_attention_f32(const float* q, const float* key_cache, const 
                                   const int64_t* position, int64_t capacity, float scale, void* workspace,
                                   int64_t workspace_bytes, float* out, hipStream_t stream);
 
+/* flux_gqa_decode_attention_f32 without a workspace argument: the split-K partials
+ * go to a fixed scratch array inside the library (201,960 bytes per GPU, held until
+ * the process ends), so the call allocates nothing -- for callers that cannot
+ * allocate (code under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  capacity must be in [1, FLUX_MAX_CAPACITY]; larger capacities are
+ * rejected with FLUX_ERROR_INVALID_VALUE.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (e.g. on two streams) race.  Results are
+ * bit-identical to flux_gqa_decode_attention_f32 (same kernels).
+ * No counterpart in the reference; added for callers that cannot allocate. */
+int flux_gqa_decode_attention_noalloc_f32(const float* q, const float* key_cache, const float* value_cache,
+                                          const int64_t* position, int64_t capacity, float scale, float* out,
+                                          hipStream_t stream);
+
 /* out[rows] = W[rows, 576] x[576] (+ residual[rows] if non-NULL).
  * Replaces the cuBLASLt o_proj GEMV (native_decode_runtime_cuda.cu:271-276) and
  * residual add. */
