@@ -50,10 +50,11 @@ constexpr int kThreads = 512;
 constexpr int kWavesPerWG = kThreads / kWave;
 constexpr int kAttnRows = 224;            // attention rows per workgroup (LDS-resident K/V)
 constexpr int kLmBatch = 4;
-// A wait that has lasted this long also watches the device error word, so one
-// workgroup's timeout ends every other workgroup's wait at once instead of
-// each of them timing out in turn (20 us of the 100 MHz wall clock; normal
-// exchanges complete in 1-10 us and never reach it).
+// A wait that has lasted this long (or its bound, if shorter) starts watching the
+// device error word (so one workgroup's timeout ends every other workgroup's wait at
+// once instead of each of them timing out in turn) and its own bound: 20 us of the
+// 100 MHz wall clock.  Normal exchanges complete in 1-10 us and never reach it, so
+// the poll loop of a normal wait does nothing but poll.
 constexpr uint64_t kWatchErrorTicks = 2000;
 
 // ---------------------------------------------------------------------------
@@ -68,6 +69,46 @@ __device__ __forceinline__ void ll_store(uint64_t* p, float v, uint32_t epoch) {
 
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// LL arena layout (uint64 words), two parities (layer parity / token parity).
+//
+// The vectors every workgroup reads (q/k/v, merged attention, r, SwiGLU output, h,
+// argmax candidates) are written in kReplicas copies, one per XCD: the workgroups of
+// XCD x poll copy x, so each cache line is polled by the 32 CUs of one XCD instead of
+// all 256.  Sixteen producers share each 128-byte line of a copy; with one copy, a
+// 256-reader exchange of such lines took 2.0 us per round on MI355X, with one copy per
+// XCD 1.4 us.  The attention partials are read by a few merge workgroups only and
+// have one copy.
+struct LLLayout {
+    static constexpr int kQkv = 0;                                        // 960
+    static constexpr int kAttnMerged = 1024;                              // 576
+    static constexpr int kResid = 1024 + 640;                             // 576 (r)
+    static constexpr int kSwiglu = 1024 + 1280;                           // 1536
+    static constexpr int kHidden = 1024 + 1280 + 1536;                    // 576 (h)
+    static constexpr int kArgmax = kHidden + 640;                         // 2 * 1024
+    static constexpr int kVectorWords = kArgmax + 2048;
+    static constexpr int kReplicas = 8;
+    // Copies start 32 words (256 bytes) apart beyond the vector block, so that equal
+    // offsets of different copies do not fall on the same memory channel.
+    static constexpr int kReplicaStride = kVectorWords + 32;
+    static constexpr int kPartials = kReplicas * kReplicaStride;          // 3 * chunks * 3 * 66
+    static constexpr int kPartialWords = kKVHeads * kMaxAttnChunks * kGroup * (kHeadDim + 2);
+    static constexpr int kParity = kPartials + kPartialWords + 64;
+    static constexpr int kTotal = 2 * kParity;
+};
+
+// Stores v into word i of every copy of a replicated vector (lane r writes copy r);
+// v must be the same in lanes 0 .. kReplicas-1.
+__device__ __forceinline__ void ll_store_replicas(uint64_t* copy0, int i, float v, uint32_t epoch, int lane) {
+    if (lane < LLLayout::kReplicas) ll_store(copy0 + lane * LLLayout::kReplicaStride + i, v, epoch);
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+    return x;
 }
 
 // Bounded waiting.  A workgroup whose wait exceeds the limit records an error
@@ -85,6 +126,7 @@ struct WaitCtx {
     int* abort;                // LDS flag shared by the workgroup
     int32_t* error;            // device error word
     const WaitShared* shared;  // LDS
+    uint64_t watch;            // min(kWatchErrorTicks, bound): when a wait starts checking
 };
 
 __device__ __noinline__ void record_error(int32_t* error, int32_t* host_error, int32_t code) {
@@ -97,19 +139,19 @@ __device__ __noinline__ void ll_timeout(int* abort, int32_t* error, const WaitSh
     record_error(error, shared->host_error, 1);
 }
 
-// true when the wait must stop: the workgroup already aborted, the device error
-// word is set (checked once the wait is long), or the wait exceeded its bound.
+// true when a wait that has lasted w.watch ticks must stop: the device error word is
+// set, or the wait exceeded its bound.
 __device__ __forceinline__ bool wait_expired(const WaitCtx& w, uint64_t start) {
-    if (*w.abort) return true;
     const uint64_t waited = wall_clock64() - start;
-    if (waited > kWatchErrorTicks &&
-        __hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-        *w.abort = 1;
-        return true;
-    }
-    if (waited > w.shared->limit) {
-        ll_timeout(w.abort, w.error, w.shared);
-        return true;
+    if (waited > w.watch) {
+        if (__hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            *w.abort = 1;
+            return true;
+        }
+        if (waited > w.shared->limit) {
+            ll_timeout(w.abort, w.error, w.shared);
+            return true;
+        }
     }
     return false;
 }
@@ -124,32 +166,18 @@ __device__ __forceinline__ void ll_fetch(const uint64_t* __restrict__ base, cons
 #pragma unroll
     for (int j = 0; j < N; ++j) ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
     if (!ready) {
-        // Two staggered polls are kept in flight so a newly published word is seen
-        // about half a memory round trip sooner than with one poll at a time.
+        // One poll per word in flight, re-issued as soon as it returns stale: polls compete
+        // with the producers' stores and with each other at the memory side, so keeping
+        // more of them in flight, or sleeping between them, makes the exchange slower.
         const uint64_t start = wall_clock64();
         while (true) {
             if (*w.abort) break;
-            uint64_t first[N], second[N];
 #pragma unroll
             for (int j = 0; j < N; ++j)
-                first[j] = static_cast<uint32_t>(word[j] >> 32) == epoch ? word[j] : ll_load(base + idx[j]);
-            __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-            for (int j = 0; j < N; ++j)
-                second[j] = static_cast<uint32_t>(word[j] >> 32) == epoch ? word[j] : ll_load(base + idx[j]);
+                if (static_cast<uint32_t>(word[j] >> 32) != epoch) word[j] = ll_load(base + idx[j]);
             ready = true;
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                if (static_cast<uint32_t>(first[j] >> 32) == epoch) word[j] = first[j];
-                ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
-            }
-            if (ready) break;
-            ready = true;
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                if (static_cast<uint32_t>(second[j] >> 32) == epoch) word[j] = second[j];
-                ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
-            }
+            for (int j = 0; j < N; ++j) ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
             if (ready) break;
             if (wait_expired(w, start)) break;
         }
@@ -188,6 +216,20 @@ struct LLOut {
     uint64_t* p;
     uint32_t epoch;
     __device__ __forceinline__ void put(int i, float v) const { ll_store(p + i, v, epoch); }
+};
+
+// QKV outputs: `v` is the same in every lane; the LL form writes every copy of the
+// replicated q/k/v vector (p = copy 0), the plain form writes once from lane 0.
+struct QkvPlainOut {
+    float* p;
+    __device__ __forceinline__ void put(int lane, int i, float v) const {
+        if (lane == 0) p[i] = v;
+    }
+};
+struct QkvLLOut {
+    uint64_t* p;
+    uint32_t epoch;
+    __device__ __forceinline__ void put(int lane, int i, float v) const { ll_store_replicas(p, i, v, epoch, lane); }
 };
 
 template <class In>
@@ -287,9 +329,10 @@ __device__ __forceinline__ RopePair rope_pair(const float* __restrict__ cos_row,
 // Normalised QKV row pair of one unit.  The RMS scale multiplies the finished dot
 // products, q = inv_rms * sum_j (h_j * wn_j) * w_j, so the sum of squares and both
 // dot products reduce at the same time (one reduction latency instead of two);
-// the reductions end in wave-uniform values.  RoPE (products rounded separately,
-// packed_qkv_rope_cache_cuda.cu:40-48) and routing as the reference: q -> out[r],
-// k/v -> the cache row at the current position (and out[r]).  Lane 0 writes.
+// the reductions end in wave-uniform values, so every lane holds the outputs.
+// RoPE (products rounded separately, packed_qkv_rope_cache_cuda.cu:40-48) and
+// routing as the reference: q -> out[r], k/v -> the cache row at the current
+// position (lane 0 writes it) and out[r] (the output policy picks the lanes).
 template <class QOut>
 __device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const float (&h)[9], const float (&wn)[9],
                                                  float eps, int unit, int lane, const RopePair& rp,
@@ -308,7 +351,6 @@ __device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const 
     ss = wave_sum_uniform(ss);
     pa = wave_sum_uniform(pa);
     pb = wave_sum_uniform(pb);
-    if (lane != 0) return;
     const float inv = rms_inverse(ss, kHidden, eps);
     const float a = pa * inv;
     const float b = pb * inv;
@@ -320,7 +362,7 @@ __device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const 
         lo = a;
         hi = b;
     }
-    if (head >= kQHeads) {
+    if (head >= kQHeads && lane == 0) {
         const bool is_key = head < kQHeads + kKVHeads;
         const int g = is_key ? head - kQHeads : head - kQHeads - kKVHeads;
         float* row = (is_key ? key_row_base : value_row_base) + g * head_stride;
@@ -328,8 +370,8 @@ __device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const 
         __hip_atomic_store(row + d, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(row + d + 32, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    out.put(r0, lo);
-    out.put(r1, hi);
+    out.put(lane, r0, lo);
+    out.put(lane, r1, hi);
 }
 
 // ---------------------------------------------------------------------------
@@ -686,21 +728,6 @@ __device__ __forceinline__ void wg_argmax(float& v, int64_t& i, float* red_v, in
     __syncthreads();
 }
 
-// ---------------------------------------------------------------------------
-// LL arena layout (uint64 words), two parities (layer parity / token parity).
-struct LLLayout {
-    static constexpr int kQkv = 0;                                        // 960
-    static constexpr int kAttnMerged = 1024;                              // 576
-    static constexpr int kResid = 1024 + 640;                             // 576 (r)
-    static constexpr int kSwiglu = 1024 + 1280;                           // 1536
-    static constexpr int kHidden = 1024 + 1280 + 1536;                    // 576 (h)
-    static constexpr int kArgmax = kHidden + 640;                         // 2 * 1024
-    static constexpr int kPartials = kArgmax + 2048;                      // 3 * chunks * 3 * 66
-    static constexpr int kPartialWords = kKVHeads * kMaxAttnChunks * kGroup * (kHeadDim + 2);
-    static constexpr int kParity = kPartials + kPartialWords + 64;
-    static constexpr int kTotal = 2 * kParity;
-};
-
 __device__ __forceinline__ uint32_t epoch_of(uint32_t token_counter, int stage) {
     // stage 0..29 = layers, 30 = argmax.  Never 0 for any token (memory starts zeroed).
     return token_counter * 32u + static_cast<uint32_t>(stage) + 1u;
@@ -810,6 +837,8 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     const int wave = tid_opaque() >> 6;
     const int G = gridDim.x;
     const int wg = blockIdx.x;
+    // This workgroup polls the copy of the replicated vectors that belongs to its XCD.
+    const int replica = static_cast<int>(xcc_id() % LLLayout::kReplicas) * LLLayout::kReplicaStride;
     const int gw = wave * G + wg;        // global wave id, interleaved across CUs
     const int chunks = G / kKVHeads < kMaxAttnChunks ? G / kKVHeads : kMaxAttnChunks;
     const int64_t cap = args.capacity;
@@ -827,7 +856,8 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     int64_t position = *args.position;
     int64_t step = *args.generation_step;
     __syncthreads();
-    const WaitCtx wctx{&abort_flag, args.error, &wait_shared};
+    const WaitCtx wctx{&abort_flag, args.error, &wait_shared,
+                       args.wait_ticks < kWatchErrorTicks ? args.wait_ticks : kWatchErrorTicks};
 
     int t = 0;
     for (; t < args.steps; ++t) {
@@ -869,7 +899,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 if (layer == 0) {
                     for (int k = tid_opaque(); k < kHidden; k += kThreads) hvec[k] = token_ok ? emb_row[k] : 0.0f;
                 } else {
-                    wg_ll_fetch<2>(ll_prev + LLLayout::kHidden, kHidden, Contiguous{}, epoch_of(counter, layer - 1),
+                    wg_ll_fetch<2>(ll_prev + replica + LLLayout::kHidden, kHidden, Contiguous{}, epoch_of(counter, layer - 1),
                                    wctx, hvec);
                 }
                 __syncthreads();
@@ -878,7 +908,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     float h[9];
                     lds_slice576(hvec, lane, h);
                     qkv_unit_compute(w, h, wn, Lw.eps, gw, lane, rp, key_layer + position * kHeadDim,
-                                     value_layer + position * kHeadDim, head_stride, LLOut{ll + LLLayout::kQkv, ep});
+                                     value_layer + position * kHeadDim, head_stride, QkvLLOut{ll + LLLayout::kQkv, ep});
                 }
             }
 
@@ -903,7 +933,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 const int qbase = g * kGroup * kHeadDim;
                 const int kbase = kQHeads * kHeadDim + g * kHeadDim;
                 wg_ll_fetch_to<1>(
-                    ll + LLLayout::kQkv, has_current ? kGroup * kHeadDim + 2 * kHeadDim : kGroup * kHeadDim,
+                    ll + replica + LLLayout::kQkv, has_current ? kGroup * kHeadDim + 2 * kHeadDim : kGroup * kHeadDim,
                     [=](int k) {
                         return k < kGroup * kHeadDim
                                    ? qbase + k
@@ -971,13 +1001,17 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     red[kWavesPerWG * 16 + wave * 16 + lane] = L;
                 }
                 __syncthreads();
-                if (tid_opaque() < 16) {
+                // Thread (copy r = t / 16, dim d = t % 16) writes dim d of copy r.
+                if (tid_opaque() < 16 * LLLayout::kReplicas) {
+                    const int dd = tid_opaque() & 15;
+                    const int r = tid_opaque() >> 4;
                     float acc = 0.0f, lsum = 0.0f;
                     for (int w = 0; w < kWavesPerWG; ++w) {
-                        acc += red[w * 16 + tid_opaque()];
-                        lsum += red[kWavesPerWG * 16 + w * 16 + tid_opaque()];
+                        acc += red[w * 16 + dd];
+                        lsum += red[kWavesPerWG * 16 + w * 16 + dd];
                     }
-                    ll_store(ll + LLLayout::kAttnMerged + h * kHeadDim + 16 * quarter + tid_opaque(), acc / lsum, ep);
+                    ll_store(ll + r * LLLayout::kReplicaStride + LLLayout::kAttnMerged + h * kHeadDim + 16 * quarter + dd,
+                             acc / lsum, ep);
                 }
                 __syncthreads();
             }
@@ -988,14 +1022,14 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 const bool active = gw < kHidden;
                 float w[9];
                 if (active) load_row576(Lw.o_proj + static_cast<int64_t>(gw) * kHidden, lane, w);
-                wg_ll_fetch<2>(ll + LLLayout::kAttnMerged, kHidden, Contiguous{}, ep, wctx, vec);
+                wg_ll_fetch<2>(ll + replica + LLLayout::kAttnMerged, kHidden, Contiguous{}, ep, wctx, vec);
                 __syncthreads();
                 FLUX_TRACE_POINT(7);
                 if (active) {
                     float a[9];
                     lds_slice576(vec, lane, a);
                     const float dot = wave_sum_uniform(dot_lane<9>(a, w));
-                    if (lane == 0) ll_store(ll + LLLayout::kResid + gw, hvec[gw] + dot, ep);
+                    ll_store_replicas(ll + LLLayout::kResid, gw, hvec[gw] + dot, ep, lane);
                 }
                 __syncthreads();
             }
@@ -1010,7 +1044,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     load_slice576(Lw.post_norm, lane, wn);
                 }
                 FLUX_TRACE_POINT(8);
-                wg_ll_fetch<2>(ll + LLLayout::kResid, kHidden, Contiguous{}, ep, wctx, rvec);
+                wg_ll_fetch<2>(ll + replica + LLLayout::kResid, kHidden, Contiguous{}, ep, wctx, rvec);
                 __syncthreads();
                 FLUX_TRACE_POINT(9);
                 if (active) {
@@ -1028,10 +1062,8 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     ss = wave_sum_uniform(ss);
                     pg = wave_sum_uniform(pg);
                     pu = wave_sum_uniform(pu);
-                    if (lane == 0) {
-                        const float inv = rms_inverse(ss, kHidden, Lw.eps);
-                        ll_store(ll + LLLayout::kSwiglu + gw, silu(pg * inv) * (pu * inv), ep);
-                    }
+                    const float inv = rms_inverse(ss, kHidden, Lw.eps);
+                    ll_store_replicas(ll + LLLayout::kSwiglu, gw, silu(pg * inv) * (pu * inv), ep, lane);
                 }
                 __syncthreads();
                 FLUX_TRACE_POINT(12);
@@ -1043,7 +1075,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 float w[24];
                 if (active) load_row1536(Lw.down + static_cast<int64_t>(gw) * kInter, lane, w);
                 FLUX_TRACE_POINT(10);
-                wg_ll_fetch<3>(ll + LLLayout::kSwiglu, kInter, Contiguous{}, ep, wctx, vec);
+                wg_ll_fetch<3>(ll + replica + LLLayout::kSwiglu, kInter, Contiguous{}, ep, wctx, vec);
                 __syncthreads();
                 FLUX_TRACE_POINT(11);
                 if (active) {
@@ -1051,7 +1083,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
 #pragma unroll
                     for (int j = 0; j < 24; ++j) sv[j] = vec[slice1536_index(lane, j)];
                     const float dot = wave_sum_uniform(dot_lane<24>(sv, w));
-                    if (lane == 0) ll_store(ll + LLLayout::kHidden + gw, rvec[gw] + dot, ep);
+                    ll_store_replicas(ll + LLLayout::kHidden, gw, rvec[gw] + dot, ep, lane);
                 }
                 __syncthreads();
             }
@@ -1062,7 +1094,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             const uint32_t ep_last = epoch_of(counter, kLayers - 1);
             const uint32_t ep_arg = epoch_of(counter, kLayers);
             const uint64_t* ll_last = args.ll + ((kLayers - 1) & 1) * LLLayout::kParity;
-            uint64_t* ll_arg = args.ll + (t & 1) * LLLayout::kParity + LLLayout::kArgmax;
+            uint64_t* ll_arg = args.ll + (t & 1) * LLLayout::kParity + LLLayout::kArgmax;  // copy 0
             const int TW = G * kWavesPerWG;
             const int64_t per = (args.vocab + TW - 1) / TW;
             const int64_t row0 = per * gw < args.vocab ? per * gw : args.vocab;
@@ -1074,7 +1106,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             float wn[9];
             load_slice576(args.final_norm, lane, wn);
             lm_load(args.lm_head, row0, row1, lane, wl);
-            wg_ll_fetch<2>(ll_last + LLLayout::kHidden, kHidden, Contiguous{}, ep_last, wctx, hvec);
+            wg_ll_fetch<2>(ll_last + replica + LLLayout::kHidden, kHidden, Contiguous{}, ep_last, wctx, hvec);
             __syncthreads();
             FLUX_TRACE_POINT(1);
             float h[9], x[9];
@@ -1094,9 +1126,12 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             // rows are read by later tokens only, from lines no CU has cached yet.
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            if (tid_opaque() == 0) {
-                ll_store(ll_arg + 2 * wg, best_v, ep_arg);
-                ll_store(ll_arg + 2 * wg + 1, __int_as_float(static_cast<int>(best_i)), ep_arg);
+            if (wave == 0) {
+                // The workgroup's candidate (valid in thread 0) goes to every copy.
+                const float cand_v = __shfl(best_v, 0, kWave);
+                const int cand_i = __shfl(static_cast<int>(best_i), 0, kWave);
+                ll_store_replicas(ll_arg, 2 * wg, cand_v, ep_arg, lane);
+                ll_store_replicas(ll_arg, 2 * wg + 1, __int_as_float(cand_i), ep_arg, lane);
             }
             // Every workgroup reduces all G partials (thread t < G reads partial t).
             float v = -INFINITY;
@@ -1104,7 +1139,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             if (static_cast<int>(tid_opaque()) < G) {
                 const int idx[2] = {2 * static_cast<int>(tid_opaque()), 2 * static_cast<int>(tid_opaque()) + 1};
                 float pv[2];
-                LLIn{ll_arg, ep_arg, wctx}.fetch(idx, pv);
+                LLIn{ll_arg + replica, ep_arg, wctx}.fetch(idx, pv);
                 v = pv[0];
                 i = static_cast<int64_t>(__float_as_int(pv[1]));
             }
@@ -1175,7 +1210,7 @@ __global__ void __launch_bounds__(kThreads) qkv_rope_cache_kernel(const float* h
         qkv_unit_compute(w, h, wn, eps, unit, lane,
                          rope_pair(cos_table + position * kHeadDim, sin_table + position * kHeadDim, unit),
                          key_cache + position * kHeadDim, value_cache + position * kHeadDim, capacity * kHeadDim,
-                         PlainOut{q_out});
+                         QkvPlainOut{q_out});
     }
 }
 
