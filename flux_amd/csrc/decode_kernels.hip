@@ -728,6 +728,33 @@ __device__ __forceinline__ void wg_argmax(float& v, int64_t& i, float* red_v, in
     __syncthreads();
 }
 
+// One argmax step against the candidate a DPP move brings in (partner lanes outside
+// the move's row mask see the identity -inf / INT_MAX, which never wins).
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ void argmax_dpp_step(float& v, int& i) {
+    const float ov = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), kCtrl, kRowMask, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(INT32_MAX, i, kCtrl, kRowMask, 0xF, false);
+    if (argmax_precedes(ov, oi, v, i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+// Wave argmax (NaN first, then larger value, then lower index) with DPP row moves and
+// row broadcasts, ending in a wave-uniform result read from lane 63: no LDS crossbar
+// (a 64-bit __shfl_xor butterfly costs 18 dependent ds_bpermute round trips).
+__device__ __forceinline__ void wave_argmax_uniform(float& v, int& i) {
+    argmax_dpp_step<kDppRowRor8, 0xF>(v, i);
+    argmax_dpp_step<kDppRowRor4, 0xF>(v, i);
+    argmax_dpp_step<kDppQuadXor2, 0xF>(v, i);
+    argmax_dpp_step<kDppQuadXor1, 0xF>(v, i);
+    argmax_dpp_step<kDppRowBcast15, 0xA>(v, i);
+    argmax_dpp_step<kDppRowBcast31, 0xC>(v, i);
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    i = __builtin_amdgcn_readlane(i, 63);
+}
+
 __device__ __forceinline__ uint32_t epoch_of(uint32_t token_counter, int stage) {
     // stage 0..29 = layers, 30 = argmax.  Never 0 for any token (memory starts zeroed).
     return token_counter * 32u + static_cast<uint32_t>(stage) + 1u;
@@ -827,7 +854,6 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     __shared__ __align__(16) float attn_pl[kAttnPlFloats];
     __shared__ int64_t red_i[kWavesPerWG];
     __shared__ float red_v[kWavesPerWG];
-    __shared__ int64_t token_shared;
     __shared__ float hvec[kHidden];   // layer input h (residual of C)
     __shared__ float rvec[kHidden];   // post-attention residual r (residual of E)
     __shared__ __align__(16) float vec[kInter];  // attention output / SwiGLU output / q of the group
@@ -1101,13 +1127,18 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             const int64_t row1 = row0 + per < args.vocab ? row0 + per : args.vocab;
             [[maybe_unused]] const int layer = kLayers;  // read by the trace points
             FLUX_TRACE_POINT(0);
-            // The first kLmBatch rows of this wave are loaded before waiting for h.
             float wl[kLmBatch][9];
             float wn[9];
             load_slice576(args.final_norm, lane, wn);
-            lm_load(args.lm_head, row0, row1, lane, wl);
             wg_ll_fetch<2>(ll_last + replica + LLLayout::kHidden, kHidden, Contiguous{}, ep_last, wctx, hvec);
+            // This token's K/V cache rows were written through (agent-scope stores, the last of
+            // them in layer 29's QKV phase); every wave waits until its stores are acknowledged
+            // before the workgroup signals its argmax candidate, so the next token's attention
+            // reads them from memory.  Here nothing but those stores and the h poll are
+            // outstanding; the logits stores issued below are not waited for.
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
+            lm_load(args.lm_head, row0, row1, lane, wl);
             FLUX_TRACE_POINT(1);
             float h[9], x[9];
             lds_slice576(hvec, lane, h);
@@ -1121,11 +1152,6 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             if (wg == 0 && tid_opaque() == 0)
                 step_error = __hip_atomic_load(args.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             FLUX_TRACE_POINT(2);
-            // This token's K/V cache rows were written through (agent-scope stores); wait
-            // until every wave's stores are acknowledged before signalling the argmax.  The
-            // rows are read by later tokens only, from lines no CU has cached yet.
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
             if (wave == 0) {
                 // The workgroup's candidate (valid in thread 0) goes to every copy.
                 const float cand_v = __shfl(best_v, 0, kWave);
@@ -1133,30 +1159,37 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 ll_store_replicas(ll_arg, 2 * wg, cand_v, ep_arg, lane);
                 ll_store_replicas(ll_arg, 2 * wg + 1, __int_as_float(cand_i), ep_arg, lane);
             }
-            // Every workgroup reduces all G partials (thread t < G reads partial t).
-            float v = -INFINITY;
-            int64_t i = INT64_MAX;
-            if (static_cast<int>(tid_opaque()) < G) {
-                const int idx[2] = {2 * static_cast<int>(tid_opaque()), 2 * static_cast<int>(tid_opaque()) + 1};
-                float pv[2];
-                LLIn{ll_arg + replica, ep_arg, wctx}.fetch(idx, pv);
-                v = pv[0];
-                i = static_cast<int64_t>(__float_as_int(pv[1]));
-            }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(v, off, kWave);
-                const int64_t oi = __shfl_xor(i, off, kWave);
-                if (argmax_precedes(ov, oi, v, i)) {
-                    v = ov;
-                    i = oi;
+            // Every workgroup reduces all G partials: thread t < G reads partial t, each of
+            // the polling waves reduces its 64 with DPP, and every thread then reduces the
+            // waves' results from LDS in the same order (so all hold the same token).
+            const int poll_waves = (G + kWave - 1) / kWave;
+            if (wave < poll_waves) {
+                float v = -INFINITY;
+                int i = INT32_MAX;
+                if (static_cast<int>(tid_opaque()) < G) {
+                    const int idx[2] = {2 * static_cast<int>(tid_opaque()), 2 * static_cast<int>(tid_opaque()) + 1};
+                    float pv[2];
+                    LLIn{ll_arg + replica, ep_arg, wctx}.fetch(idx, pv);
+                    v = pv[0];
+                    i = __float_as_int(pv[1]);
+                }
+                wave_argmax_uniform(v, i);
+                if (lane == 0) {
+                    red_v[wave] = v;
+                    red_i[wave] = i;
                 }
             }
-            wg_argmax(v, i, red_v, red_i);
-            FLUX_TRACE_POINT(3);
-            if (tid_opaque() == 0) token_shared = (i >= 0 && i < args.vocab) ? i : 0;
             __syncthreads();
-            const int64_t next = token_shared;
+            float v = red_v[0];
+            int64_t i = red_i[0];
+            for (int w = 1; w < poll_waves; ++w) {
+                if (argmax_precedes(red_v[w], red_i[w], v, i)) {
+                    v = red_v[w];
+                    i = red_i[w];
+                }
+            }
+            FLUX_TRACE_POINT(3);
+            const int64_t next = (i >= 0 && i < args.vocab) ? i : 0;
             if (wg == 0 && tid_opaque() == 0) {
                 // A step that ran after any workgroup's wait gave up computed from stale
                 // inputs: its token is reported as -1, never as a plausible id.
