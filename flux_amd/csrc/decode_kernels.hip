@@ -1494,9 +1494,12 @@ int max_attention_positions(int grid) {
 // Cooperative launch: the runtime refuses to start a grid whose workgroups cannot all be
 // resident at once (hipErrorCooperativeLaunchTooLarge), instead of letting the resident
 // ones wait for the rest until their bounded waits expire.
-hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream) {
+hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream, bool cooperative) {
     DecodeArgs copy = args;
     void* params[] = {&copy};
+    if (!cooperative)
+        return hipLaunchKernel(reinterpret_cast<const void*>(fused_decode_kernel), dim3(grid), dim3(kThreads), params,
+                               fused_decode_dynamic_lds(), stream);
     return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fused_decode_kernel), dim3(grid), dim3(kThreads),
                                       params, static_cast<unsigned int>(fused_decode_dynamic_lds()), stream);
 }

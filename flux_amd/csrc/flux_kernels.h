@@ -44,7 +44,9 @@ int fused_decode_threads();
 size_t fused_decode_dynamic_lds();
 int max_attention_positions(int grid);
 hipError_t fused_decode_occupancy(int* blocks_per_cu);
-hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream);
+// cooperative = false launches it plainly (profiling: rocprofv3 7.2 crashes at exit after
+// cooperative launches); the occupancy check and the bounded waits remain the guard.
+hipError_t launch_fused_decode(const DecodeArgs& args, int grid, hipStream_t stream, bool cooperative = true);
 void* fused_decode_function();
 
 // ---- isolated decode phases ----

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace flux {
@@ -143,6 +144,8 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
                              const CacheSources& sources, const double* epsilons, const double* scales,
                              hipStream_t stream)
     : capacity_(capacity), start_position_(position), rope_cos_(rope_cos), rope_sin_(rope_sin) {
+    const char* plain = std::getenv("FLUX_DECODE_PLAIN_LAUNCH");
+    cooperative_ = plain == nullptr || plain[0] == '\0' || std::strcmp(plain, "0") == 0;
     validate_weights(weights, "flux native full decode");
     validate_scalars(epsilons, scales, "flux native full decode");
     if (capacity < 1 || capacity > kMaxCapacity)
@@ -189,7 +192,7 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
         check_hip(hipEventCreateWithFlags(&setup, hipEventDisableTiming), "creating setup event");
         check_hip(hipEventRecord(setup, stream), "recording setup event");
         check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
-        check_hip(launch_fused_decode(args_, grid_, capture_stream_), "warming fused decode");
+        check_hip(launch_fused_decode(args_, grid_, capture_stream_, cooperative_), "warming fused decode");
         check_hip(counted_stream_sync(capture_stream_), "warming fused decode");
         check_hip(hipEventDestroy(setup), "destroying setup event");
         if (device_error() != 0) throw FluxError(FLUX_ERROR_DEVICE, "flux native full decode: warm-up step failed");
@@ -219,7 +222,7 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
             for (hipGraphNode_t node : nodes) {
                 hipGraphNodeType type;
                 check_hip(hipGraphNodeGetType(node, &type), "reading graph node type");
-                if (type != hipGraphNodeTypeKernel) continue;
+                if (type != hipGraphNodeTypeKernel || !cooperative_) continue;
                 hipLaunchAttributeValue value{};
                 value.cooperative = 1;
                 cooperative_graph_ =
@@ -362,7 +365,7 @@ void DecodeRuntime::launch_steps(int64_t steps, hipStream_t stream, hipStream_t)
     constexpr int64_t kMaxStepsPerLaunch = 1024;
     for (int64_t done = 0; done < steps; done += kMaxStepsPerLaunch) {
         args.steps = static_cast<int>(std::min(kMaxStepsPerLaunch, steps - done));
-        check_hip(launch_fused_decode(args, grid_, stream), "launching fused decode");
+        check_hip(launch_fused_decode(args, grid_, stream, cooperative_), "launching fused decode");
     }
 }
 

@@ -103,6 +103,9 @@ private:
     int32_t* host_error_ = nullptr;         // mapped pinned host memory
     int32_t* host_error_device_ = nullptr;  // its device address
     bool cooperative_graph_ = false;
+    // Cooperative launches unless FLUX_DECODE_PLAIN_LAUNCH is set to a value other than 0
+    // (profiling runs: rocprofv3 7.2 crashes at exit after cooperative launches).
+    bool cooperative_ = true;
     LayerWeights* layers_ = nullptr;
     size_t state_bytes_ = 0;
     size_t ll_bytes_ = 0;
