@@ -296,6 +296,36 @@ def test_zero_weight_runtime_closed_form(gpu_device):
     assert runtime.device_error() == 0
 
 
+def test_fused_argmax_ties_pick_the_lowest_index(gpu_device):
+    """Argmax order of greedy_generation_cuda.cu:20-37 (ties -> lowest index, as torch.argmax):
+    the LM-head rows of the untied vocab-128 model repeat with period 8, so every step's
+    maximum is attained by 16 rows held by workgroups 8 apart.  In the fused kernel's argmax
+    exchange those candidates meet in DPP row moves (8 lanes apart), row broadcasts (16, 32)
+    and across polling waves (64), and the winner must be the class's lowest row (< 8).  The
+    stream is checked token for token against the oracle on the same weights."""
+    from flux_amd.model import FINAL_FLUX_OPERATOR_CATEGORIES, enable_flux_ops
+
+    spec = synthetic.SyntheticSpec(seed=2701, vocab=128, permuted_head_seed=31, embedding_scale=50.0)
+    state = synthetic.synthetic_state_dict(spec)
+    state["lm_head.weight"] = state["lm_head.weight"][torch.arange(128) % 8].contiguous()
+    model = synthetic.build_hf_model(spec, device=gpu_device)
+    with torch.no_grad():
+        model.lm_head.weight.copy_(state["lm_head.weight"])
+    enable_flux_ops(model, operators=FINAL_FLUX_OPERATOR_CATEGORIES)
+    prompt = (torch.arange(7).unsqueeze(0) * 11 + 3) % 128
+    runtime = NativeSmolLM2Prefill.capture(model, prompt.to(gpu_device), max_decode_steps=15)
+    generated = runtime.generate_greedy(16)[0].cpu().tolist()
+    logits = _decode_logits(runtime).cpu()
+    torch.cuda.synchronize()
+    assert runtime.device_error() == 0
+    expected, _, _ = OracleLlama(state).greedy(prompt, 16)
+    assert generated == expected
+    assert all(0 <= t < 8 for t in generated)
+    assert len(set(generated)) > 1, f"stream {generated} does not change; it would not test the feedback"
+    # Tied rows give bitwise-equal logits (each row's dot product is reduced in the same order).
+    assert torch.equal(logits.reshape(16, 8), logits[:8].repeat(16, 1))
+
+
 def test_decode_capture_from_hf_prefill(small_model):
     """NativeSmolLM2Decode.capture: eager HF prefill on the GPU, then native decode."""
     record = golden("small128.npz")
