@@ -17,7 +17,8 @@
 // Per layer the phases are
 //   A  norm(h) -> packed QKV GEMV -> RoPE(q,k) -> K/V cache write   (480 waves)
 //   B  split-K GQA attention partials, one (KV head, position chunk) per WG
-//   B2 merge partials per query head                                 (9 WGs)
+//      (one chunk per 64 attended positions, at most 85 per KV head)
+//   B2 merge partials per query head (36 WGs: query head x 16 dims)
 //   C  o_proj GEMV + residual                                        (576 waves)
 //   D  norm(r) -> packed gate/up GEMV -> SwiGLU                      (1536 waves)
 //   E  down GEMV + residual                                          (576 waves)
@@ -878,9 +879,16 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     }
     if (tid_opaque() < kLayers) layer_desc[tid_opaque()] = args.layers[tid_opaque()];
     const uint32_t counter0 = *args.token_counter;
-    int64_t token = *args.input_token;
-    int64_t position = *args.position;
-    int64_t step = *args.generation_step;
+    // The token state is the same for every lane: kept in scalar registers.
+    auto uniform64 = [](int64_t v) {
+        const uint64_t u = static_cast<uint64_t>(v);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    int64_t token = uniform64(*args.input_token);
+    int64_t position = uniform64(*args.position);
+    int64_t step = uniform64(*args.generation_step);
     __syncthreads();
     const WaitCtx wctx{&abort_flag, args.error, &wait_shared,
                        args.wait_ticks < kWatchErrorTicks ? args.wait_ticks : kWatchErrorTicks};
@@ -900,6 +908,12 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         const float* cos_row = args.rope_cos + position * kHeadDim;
         const float* sin_row = args.rope_sin + position * kHeadDim;
         const bool token_ok = token >= 0 && token < args.vocab;
+        // Position chunks of this token's attention: one per 64 attended positions, at most
+        // `chunks` (85 on 256 CUs, reached from 5377 positions on).  Short contexts then
+        // merge a few partials instead of 85 mostly one-row ones (ctx 128: 0.457 -> 0.427 ms
+        // per token, 1024: 0.472 -> 0.436; 64-row chunks measured faster than 32, 96 or 128).
+        const int want_chunks = static_cast<int>((attended + 63) >> 6);
+        const int tchunks = __builtin_amdgcn_readfirstlane(want_chunks < chunks ? want_chunks : chunks);
         const float* emb_row = args.embedding + (token_ok ? token : 0) * kHidden;
 
         for (int layer = 0; layer < kLayers; ++layer) {
@@ -940,11 +954,11 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
 
             // ---- B: attention partial of (KV group g, position chunk c) ----
             FLUX_TRACE_POINT(2);
-            if (wg < kKVHeads * chunks) {
+            if (wg < kKVHeads * tchunks) {
                 const int g = wg % kKVHeads;
                 const int c = wg / kKVHeads;
                 int64_t begin, end;
-                chunk_range(attended, chunks, c, begin, end);
+                chunk_range(attended, tchunks, c, begin, end);
                 const int64_t cached_end = end < position ? end : position;
                 const int cached_rows = cached_end > begin ? static_cast<int>(cached_end - begin) : 0;
                 float* k_lds = part;
@@ -978,7 +992,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 FLUX_TRACE_POINT(3);
                 attn_compute(k_lds, v_lds, vec, static_cast<int>(end - begin), Lw.scale * kLog2e,
                              AttnScratch{attn_sp, attn_pl, red},
-                             PartialLLOut{ll + LLLayout::kPartials + (g * chunks + c) * partial_stride, ep});
+                             PartialLLOut{ll + LLLayout::kPartials + (g * tchunks + c) * partial_stride, ep});
             }
 
             FLUX_TRACE_POINT(4);
@@ -989,9 +1003,9 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 const int g = h / kGroup;
                 const int hh = h % kGroup;
                 constexpr int kRun = 18;  // 16 dims + m + l per chunk
-                const uint64_t* pbase = ll + LLLayout::kPartials + g * chunks * partial_stride + hh * (kHeadDim + 2);
+                const uint64_t* pbase = ll + LLLayout::kPartials + g * tchunks * partial_stride + hh * (kHeadDim + 2);
                 wg_ll_fetch<(kMaxAttnChunks * kRun + kThreads - 1) / kThreads>(
-                    pbase, chunks * kRun,
+                    pbase, tchunks * kRun,
                     [=](int k) {
                         const int cc = k / kRun;
                         const int j = k - cc * kRun;
@@ -1003,13 +1017,13 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 // Global max of the chunk maxima: lane-strided, then wave butterfly (every wave
                 // computes the same value).
                 float M = -INFINITY;
-                for (int cc = lane; cc < chunks; cc += kWave) M = fmaxf(M, part[cc * kRun + 16]);
+                for (int cc = lane; cc < tchunks; cc += kWave) M = fmaxf(M, part[cc * kRun + 16]);
                 M = wave_max(M);
                 // Thread (slot = t / 16, d = t % 16) sums chunks cc = slot, slot + 32, ...
                 const int d = tid_opaque() & 15;
                 const int slot = tid_opaque() >> 4;
                 float O = 0.0f, L = 0.0f;
-                for (int cc = slot; cc < chunks; cc += kThreads / 16) {
+                for (int cc = slot; cc < tchunks; cc += kThreads / 16) {
                     const float* pc = part + cc * kRun;
                     const float mc = pc[16];
                     if (mc == -INFINITY) continue;
