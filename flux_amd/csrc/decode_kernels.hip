@@ -76,12 +76,14 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
 // LL arena layout (uint64 words), two parities (layer parity / token parity).
 //
 // The vectors every workgroup reads (q/k/v, merged attention, r, SwiGLU output, h,
-// argmax candidates) are written in kReplicas copies, one per XCD: the workgroups of
-// XCD x poll copy x, so each cache line is polled by the 32 CUs of one XCD instead of
-// all 256.  Sixteen producers share each 128-byte line of a copy; with one copy, a
+// argmax candidates) are written in kReplicas copies: the workgroups of XCD x poll
+// copy x % kReplicas, so each cache line is polled by the 64 CUs of two XCDs instead
+// of all 256.  Sixteen producers share each 128-byte line of a copy; with one copy, a
 // 256-reader exchange of such lines took 2.0 us per round on MI355X, with one copy per
-// XCD 1.4 us.  The attention partials are read by a few merge workgroups only and
-// have one copy.
+// XCD 1.4 us.  Measured per token at ctx 8192: 2 copies 0.461 ms, 4 copies 0.459,
+// 8 copies 0.464, 16 copies 0.499 (the stores of more copies cost more than the
+// spread polls gain).  The attention partials are read by a few merge workgroups only
+// and have one copy.
 struct LLLayout {
     static constexpr int kQkv = 0;                                        // 960
     static constexpr int kAttnMerged = 1024;                              // 576
@@ -90,7 +92,7 @@ struct LLLayout {
     static constexpr int kHidden = 1024 + 1280 + 1536;                    // 576 (h)
     static constexpr int kArgmax = kHidden + 640;                         // 2 * 1024
     static constexpr int kVectorWords = kArgmax + 2048;
-    static constexpr int kReplicas = 8;
+    static constexpr int kReplicas = 4;
     // Copies start 32 words (256 bytes) apart beyond the vector block, so that equal
     // offsets of different copies do not fall on the same memory channel.
     static constexpr int kReplicaStride = kVectorWords + 32;
@@ -172,15 +174,16 @@ __device__ __forceinline__ void ll_fetch(const uint64_t* __restrict__ base, cons
         // more of them in flight, or sleeping between them, makes the exchange slower.
         const uint64_t start = wall_clock64();
         while (true) {
-            if (*w.abort) break;
 #pragma unroll
             for (int j = 0; j < N; ++j)
                 if (static_cast<uint32_t>(word[j] >> 32) != epoch) word[j] = ll_load(base + idx[j]);
+            // The abort and time checks run while the re-polls are in flight.
+            if (*w.abort) break;
+            if (wait_expired(w, start)) break;
             ready = true;
 #pragma unroll
             for (int j = 0; j < N; ++j) ready &= static_cast<uint32_t>(word[j] >> 32) == epoch;
             if (ready) break;
-            if (wait_expired(w, start)) break;
         }
     }
 #pragma unroll
@@ -254,7 +257,7 @@ __device__ __forceinline__ void norm_slice_w(const float (&h)[9], const float (&
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < 9; ++j) ss = fmaf(h[j], h[j], ss);
-    ss = wave_sum(ss);
+    ss = wave_sum_uniform(ss);
     const float inv = rms_inverse(ss, kHidden, eps);
 #pragma unroll
     for (int j = 0; j < 9; ++j) x[j] = wn[j] * (h[j] * inv);
@@ -645,6 +648,15 @@ __device__ __forceinline__ void chunk_range(int64_t attended, int chunks, int c,
     if (begin > end) begin = end;
 }
 
+// The same in 32-bit arithmetic (attended <= the 16384-position capacity), for the
+// fused kernel, which recomputes it every layer.
+__device__ __forceinline__ void chunk_range32(int attended, int chunks, int c, int& begin, int& end) {
+    const int per = static_cast<int>((static_cast<unsigned>(attended) + chunks - 1) / static_cast<unsigned>(chunks));
+    begin = per * c;
+    end = begin + per < attended ? begin + per : attended;
+    if (begin > end) begin = end;
+}
+
 // ---------------------------------------------------------------------------
 // LM head + argmax: rows [row0, row1) for one wave, batches of kLmBatch rows.
 // Rows [row0, row1) of the LM head, kLmBatch rows per stage, two stages in
@@ -657,7 +669,7 @@ __device__ __forceinline__ void lm_stage(const float (&x)[9], const float (&w)[k
     const int lane = tid_opaque() & 63;
 #pragma unroll
     for (int r = 0; r < kLmBatch; ++r) {
-        const float v = wave_sum(dot_lane<9>(x, w[r]));
+        const float v = wave_sum_uniform(dot_lane<9>(x, w[r]));
         const int64_t row = base + r;
         if (row < row1) {
             if (lane == 0) logits.put(row, v);
@@ -864,7 +876,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     const int wave = tid_opaque() >> 6;
     const int G = gridDim.x;
     const int wg = blockIdx.x;
-    // This workgroup polls the copy of the replicated vectors that belongs to its XCD.
+    // This workgroup polls the copy of the replicated vectors that its XCD shares with one other.
     const int replica = static_cast<int>(xcc_id() % LLLayout::kReplicas) * LLLayout::kReplicaStride;
     const int gw = wave * G + wg;        // global wave id, interleaved across CUs
     const int chunks = G / kKVHeads < kMaxAttnChunks ? G / kKVHeads : kMaxAttnChunks;
@@ -913,10 +925,12 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         // merge a few partials instead of 85 mostly one-row ones (ctx 128: 0.457 -> 0.427 ms
         // per token, 1024: 0.472 -> 0.436; 64-row chunks measured faster than 32, 96 or 128).
         const int want_chunks = static_cast<int>((attended + 63) >> 6);
-        const int tchunks = __builtin_amdgcn_readfirstlane(want_chunks < chunks ? want_chunks : chunks);
+        const int tchunks_token = __builtin_amdgcn_readfirstlane(want_chunks < chunks ? want_chunks : chunks);
         const float* emb_row = args.embedding + (token_ok ? token : 0) * kHidden;
 
         for (int layer = 0; layer < kLayers; ++layer) {
+            int tchunks = tchunks_token;
+            asm volatile("" : "+s"(tchunks));
             const LayerWeights Lw = uniform_desc(layer_desc[layer]);
             const uint32_t ep = epoch_of(counter, layer);
             uint64_t* ll = args.ll + (layer & 1) * LLLayout::kParity;
@@ -957,8 +971,9 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             if (wg < kKVHeads * tchunks) {
                 const int g = wg % kKVHeads;
                 const int c = wg / kKVHeads;
-                int64_t begin, end;
-                chunk_range(attended, tchunks, c, begin, end);
+                int begin32, end32;
+                chunk_range32(static_cast<int>(attended), tchunks, c, begin32, end32);
+                const int64_t begin = begin32, end = end32;
                 const int64_t cached_end = end < position ? end : position;
                 const int cached_rows = cached_end > begin ? static_cast<int>(cached_end - begin) : 0;
                 float* k_lds = part;
@@ -1014,16 +1029,17 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     ep, wctx, part);
                 __syncthreads();
                 FLUX_TRACE_POINT(5);
-                // Global max of the chunk maxima: lane-strided, then wave butterfly (every wave
-                // computes the same value).
+                // Global max of the chunk maxima: lane-strided, then a DPP reduction into a
+                // scalar (every wave computes the same value).
                 float M = -INFINITY;
                 for (int cc = lane; cc < tchunks; cc += kWave) M = fmaxf(M, part[cc * kRun + 16]);
-                M = wave_max(M);
-                // Thread (slot = t / 16, d = t % 16) sums chunks cc = slot, slot + 32, ...
-                const int d = tid_opaque() & 15;
-                const int slot = tid_opaque() >> 4;
+                M = wave_max_uniform(M);
+                // Wave w merges dims 2w (lanes 0-31) and 2w + 1 (lanes 32-63); lane slot
+                // s = lane % 32 sums chunks s, s + 32, ...
+                const int slot = lane & 31;
+                const int d = 2 * wave + (lane >> 5);
                 float O = 0.0f, L = 0.0f;
-                for (int cc = slot; cc < tchunks; cc += kThreads / 16) {
+                for (int cc = slot; cc < tchunks; cc += 32) {
                     const float* pc = part + cc * kRun;
                     const float mc = pc[16];
                     if (mc == -INFINITY) continue;
@@ -1031,27 +1047,21 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     O = fmaf(pc[d], f, O);
                     L = fmaf(pc[17], f, L);
                 }
-                // Reduce over the 4 slots of a wave (lanes with equal d), then over waves.
-                O += __shfl_xor(O, 16, kWave);
-                O += __shfl_xor(O, 32, kWave);
-                L += __shfl_xor(L, 16, kWave);
-                L += __shfl_xor(L, 32, kWave);
-                if (lane < 16) {
-                    red[wave * 16 + lane] = O;
-                    red[kWavesPerWG * 16 + wave * 16 + lane] = L;
-                }
+                // Sum over each half: rows of 16 lanes, then row_bcast15 adds row 0 into
+                // row 1 and row 2 into row 3, so lanes 31 and 63 hold the two halves' sums.
+                O = row16_sum(O);
+                L = row16_sum(L);
+                O += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(O), kDppRowBcast15, 0xA, 0xF, false));
+                L += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), kDppRowBcast15, 0xA, 0xF, false));
+                if ((lane & 31) == 31) red[d] = O / L;
                 __syncthreads();
-                // Thread (copy r = t / 16, dim d = t % 16) writes dim d of copy r.
+                // Thread (copy r = t / 16, dim d = t % 16) writes dim d of copy r: each copy's
+                // 16 dims are one 128-byte line written by one instruction.
                 if (tid_opaque() < 16 * LLLayout::kReplicas) {
                     const int dd = tid_opaque() & 15;
                     const int r = tid_opaque() >> 4;
-                    float acc = 0.0f, lsum = 0.0f;
-                    for (int w = 0; w < kWavesPerWG; ++w) {
-                        acc += red[w * 16 + dd];
-                        lsum += red[kWavesPerWG * 16 + w * 16 + dd];
-                    }
                     ll_store(ll + r * LLLayout::kReplicaStride + LLLayout::kAttnMerged + h * kHeadDim + 16 * quarter + dd,
-                             acc / lsum, ep);
+                             red[dd], ep);
                 }
                 __syncthreads();
             }
