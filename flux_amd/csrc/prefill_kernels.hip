@@ -409,111 +409,6 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_ring_kernel(GemmArgs args) 
     gemm_epilogue<E, MI>(args, acc, m0 + wm * 32 * MI, n0 + wn * 64, lane);
 }
 
-// Narrow-column variant for the residual / plain epilogues of N = 576 outputs
-// (o_proj, down): block tile 64 x 64, 4 waves in 2 x 2, wave tile 32 x 32 (one
-// accumulator chain).  576 columns are 9 such tiles, so no wave computes a padded
-// column group, and the 9 x (M / 64) blocks are small enough for the dispatcher to
-// spread them evenly over the CUs.  A stage is 32 K values, one 128-byte line per
-// row, copied HBM -> LDS with global_load_lds into two buffers; MFMA instruction s
-// of each 16-deep half pairs K index s with s + 8, as in gemm_kernel.
-template <GemmEpilogue E>
-__global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args) {
-    static_assert(E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual, "plain epilogues only");
-    constexpr int kRows = 64;
-    constexpr int kDepth = 32;  // K values per stage: one 128-byte line per row
-    __shared__ __align__(16) float a_s0[kRows * kDepth];
-    __shared__ __align__(16) float a_s1[kRows * kDepth];
-    __shared__ __align__(16) float b_s0[kRows * kDepth];
-    __shared__ __align__(16) float b_s1[kRows * kDepth];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kRows;
-    const int n0 = blockIdx.x * kRows;
-    const int K = args.k;
-
-    // Copy j (0, 1) of wave w covers rows 8 (w + 4 j) .. + 7; lane l fills piece
-    // l % 8 of row l / 8, which holds K piece (l % 8) ^ ((row / 2) % 8): the 16 rows
-    // read by one 16-lane pass then cover all 64 banks.
-    const float* a_src[2];
-    const float* b_src[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = 8 * (wave + 4 * j) + (lane >> 3);
-        const int piece = (lane & 7) ^ ((row >> 1) & 7);
-        const int64_t ga = m0 + row < args.m ? m0 + row : args.m - 1;
-        a_src[j] = args.a + ga * K + 4 * piece;
-        b_src[j] = args.b + static_cast<int64_t>(n0 + row) * K + 4 * piece;
-    }
-    auto issue_stage = [&](int k0, float* as, float* bs) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            lds_copy16(a_src[j] + k0, as + (wave + 4 * j) * 8 * kDepth);
-            lds_copy16(b_src[j] + k0, bs + (wave + 4 * j) * 8 * kDepth);
-        }
-    };
-
-    f32x16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    // Lane reads row r, K pieces 2 h + q + 4 u (u = 16-deep half of the stage).
-    const int h = lane >> 5;
-    const int ra = wm * 32 + (lane & 31);
-    const int rb = wn * 32 + (lane & 31);
-    int a_off[4], b_off[4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            a_off[2 * u + q] = ra * kDepth + 4 * ((4 * u + 2 * h + q) ^ ((ra >> 1) & 7));
-            b_off[2 * u + q] = rb * kDepth + 4 * ((4 * u + 2 * h + q) ^ ((rb >> 1) & 7));
-        }
-    auto multiply = [&](const float* as, const float* bs) {
-        f32x4 av[4], bv[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            av[p] = *reinterpret_cast<const f32x4*>(as + a_off[p]);
-            bv[p] = *reinterpret_cast<const f32x4*>(bs + b_off[p]);
-        }
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p][kk], bv[p][kk], acc, 0, 0, 0);
-    };
-
-    const int stages = K / kDepth;
-    issue_stage(0, a_s0, b_s0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int s = 0; s < stages; s += 2) {
-        if (s + 1 < stages) issue_stage((s + 1) * kDepth, a_s1, b_s1);
-        multiply(a_s0, b_s0);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (s + 1 < stages) {
-            if (s + 2 < stages) issue_stage((s + 2) * kDepth, a_s0, b_s0);
-            multiply(a_s1, b_s1);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-        }
-    }
-
-    const int col = n0 + wn * 32 + (lane & 31);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 32 + mfma32_row(lane, r);
-        if (row >= args.m) continue;
-        const int64_t i0 = row * args.n + col;
-        if constexpr (E == GemmEpilogue::kResidual) {
-            args.c[i0] = args.residual[i0] + acc[r];
-        } else {
-            args.c[i0] = acc[r];
-        }
-    }
-}
-
 // Grids smaller than the device (short and mid-length prompts): one block per
 // (32 * RT) x 64 output tile, RT = 1, 2 or 4.  Its kSplitWaves waves are RT row tiles
 // of 32 times kSplitWaves / RT contiguous K ranges.  A wave streams its 32 A rows and the
@@ -750,11 +645,17 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     }
 }
 
-// gemm_narrow_kernel for grids smaller than the device: the same 64 x 64 tiles and
-// 32-deep stages through a ring of four buffers (three copies in flight), stepped as
-// in gemm_ring_kernel.
+// Narrow-column GEMM for the residual / plain epilogues of N = 576 outputs (o_proj,
+// down): block tile 64 x 64, 4 waves in 2 x 2, wave tile 32 x 32 (one accumulator
+// chain).  576 columns are 9 such tiles, so no wave computes a padded column group,
+// and the 9 x (M / 64) blocks are small enough to spread evenly over the CUs.  A
+// stage is 32 K values, one 128-byte line per row (16-byte pieces XOR-swizzled so a
+// 16-lane read pass covers all 64 banks), streamed through a ring of four LDS buffers
+// with three copies in flight, stepped as in gemm_ring_kernel.  For every grid size:
+// at 8192 rows the ring measured 0.3 ms per prefill faster than two buffers (which
+// fit more blocks per CU but wait on each stage's copy).
 template <GemmEpilogue E>
-__global__ void __launch_bounds__(kGemmThreads) gemm_narrow_ring_kernel(GemmArgs args) {
+__global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args) {
     static_assert(E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual, "plain epilogues only");
     constexpr int kNS = 4;
     constexpr int kRows = 64;
@@ -1294,7 +1195,7 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 
 }  // namespace
 
-// Grids below this many blocks (fewer than the device's CUs) use the ring kernels.
+// Grids below this many blocks (fewer than the device's CUs) use the ring kernel.
 constexpr int64_t kRingBlocks = 256;
 constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
 
@@ -1391,22 +1292,11 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         args.k % 32 == 0) {
         // Column counts that are not a multiple of 128 (576): 64 x 64 tiles.
         const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
-        const bool small = static_cast<int64_t>(grid.x) * grid.y < kRingBlocks;
-        if (epilogue == GemmEpilogue::kResidual) {
-            if (small)
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_ring_kernel<GemmEpilogue::kResidual>), grid, block, 0,
-                                   stream, args);
-            else
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kResidual>), grid, block, 0,
-                                   stream, args);
-        } else {
-            if (small)
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_ring_kernel<GemmEpilogue::kStore>), grid, block, 0,
-                                   stream, args);
-            else
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kStore>), grid, block, 0, stream,
-                                   args);
-        }
+        if (epilogue == GemmEpilogue::kResidual)
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kResidual>), grid, block, 0, stream,
+                               args);
+        else
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kStore>), grid, block, 0, stream, args);
         return hipGetLastError();
     }
     // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles;
