@@ -384,6 +384,40 @@ def test_odd_length_prefill_matches_oracle(small_model, length):
         torch.testing.assert_close(v, cache.values[layer][0][:, positions], rtol=KV_RTOL, atol=KV_ATOL)
 
 
+def test_decode_across_empty_position_chunks(small_model):
+    """Decode steps whose attended lengths (5439 .. 5462) straddle 5441 .. 5460, where 85 position
+    chunks of ceil(L / 85) rows leave the last chunk empty: its partial (m = -inf, l = 0) must drop
+    out of the merge.  Teacher-forced changing tokens through replay(), logits against the CPU
+    oracle at every step, and the last step's K/V rows of every layer."""
+    prompt_len, steps = 5438, 24
+    g = torch.Generator().manual_seed(5441)
+    prompt = torch.randint(0, 128, (1, prompt_len), generator=g)
+    fed = torch.randint(0, 128, (steps,), generator=g)
+    runtime = NativeSmolLM2Prefill.capture(small_model, prompt.cuda(), max_decode_steps=steps)
+    torch.cuda.synchronize()
+    oracle = OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=2701, vocab=128)))
+    cache = OracleCache()
+    with torch.inference_mode():
+        expected = oracle.forward(prompt, cache)[0, -1]
+    torch.testing.assert_close(runtime.logits[0, 0].float().cpu(), expected, atol=LOGIT_ATOL, rtol=LOGIT_RTOL)
+    for step in range(steps):
+        token = int(fed[step])
+        logits = runtime.replay(torch.tensor([[token]], dtype=torch.long, device="cuda"))
+        torch.cuda.synchronize()
+        with torch.inference_mode():
+            expected = oracle.forward(torch.tensor([[token]]), cache)[0, -1]
+        torch.testing.assert_close(logits[0, 0].float().cpu(), expected, atol=LOGIT_ATOL, rtol=LOGIT_RTOL,
+                                   msg=lambda m: f"step {step} (attended {prompt_len + step + 1}): {m}")
+    pos = prompt_len + steps - 1
+    assert runtime.cache_position == pos + 1
+    for layer in range(30):
+        torch.testing.assert_close(runtime.key_cache[layer, 0][:, pos].float().cpu(), cache.keys[layer][0][:, pos],
+                                   rtol=KV_RTOL, atol=KV_ATOL)
+        torch.testing.assert_close(runtime.value_cache[layer, 0][:, pos].float().cpu(),
+                                   cache.values[layer][0][:, pos], rtol=KV_RTOL, atol=KV_ATOL)
+    assert runtime.device_error() == 0
+
+
 def test_wait_timeout_reports_error_and_invalid_tokens(small_model):
     """Failure handling, forced from the host: a zero bound on the fused kernel's
     cross-workgroup waits makes them give up at once (every kernel still exits normally).
