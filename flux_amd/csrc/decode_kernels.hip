@@ -311,11 +311,12 @@ __device__ __forceinline__ void qkv_unit_rows(int unit, int& head, int& d, int& 
     r1 = r0 + 32;
 }
 
+template <bool kStream = false>
 __device__ __forceinline__ void qkv_load(const float* __restrict__ qkv_w, int unit, int lane, QkvUnitWeights& w) {
     int head, d, r0, r1;
     qkv_unit_rows(unit, head, d, r0, r1);
-    load_row576(qkv_w + static_cast<int64_t>(r0) * kHidden, lane, w.w0);
-    load_row576(qkv_w + static_cast<int64_t>(r1) * kHidden, lane, w.w1);
+    load_row576<kStream>(qkv_w + static_cast<int64_t>(r0) * kHidden, lane, w.w0);
+    load_row576<kStream>(qkv_w + static_cast<int64_t>(r1) * kHidden, lane, w.w1);
 }
 
 // Computes the unit's two rows and routes them: q -> q_out[h*64+d], k -> cache
@@ -954,7 +955,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 float wn[9];
                 RopePair rp{};
                 if (active) {
-                    qkv_load(Lw.qkv, gw, lane, w);
+                    qkv_load<true>(Lw.qkv, gw, lane, w);
                     load_slice576(Lw.input_norm, lane, wn);
                     rp = rope_pair(cos_row, sin_row, gw);
                 }
@@ -1079,7 +1080,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 FLUX_TRACE_POINT(6);
                 const bool active = gw < kHidden;
                 float w[9];
-                if (active) load_row576(Lw.o_proj + static_cast<int64_t>(gw) * kHidden, lane, w);
+                if (active) load_row576<true>(Lw.o_proj + static_cast<int64_t>(gw) * kHidden, lane, w);
                 wg_ll_fetch<2>(ll + replica + LLLayout::kAttnMerged, kHidden, Contiguous{}, ep, wctx, vec);
                 __syncthreads();
                 FLUX_TRACE_POINT(7);
@@ -1097,8 +1098,8 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 const bool active = gw < kInter;
                 float wg_[9], wu[9], wn[9];
                 if (active) {
-                    load_row576(Lw.gate_up + static_cast<int64_t>(gw) * kHidden, lane, wg_);
-                    load_row576(Lw.gate_up + static_cast<int64_t>(kInter + gw) * kHidden, lane, wu);
+                    load_row576<true>(Lw.gate_up + static_cast<int64_t>(gw) * kHidden, lane, wg_);
+                    load_row576<true>(Lw.gate_up + static_cast<int64_t>(kInter + gw) * kHidden, lane, wu);
                     load_slice576(Lw.post_norm, lane, wn);
                 }
                 FLUX_TRACE_POINT(8);
@@ -1131,7 +1132,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             {
                 const bool active = gw < kHidden;
                 float w[24];
-                if (active) load_row1536(Lw.down + static_cast<int64_t>(gw) * kInter, lane, w);
+                if (active) load_row1536<true>(Lw.down + static_cast<int64_t>(gw) * kInter, lane, w);
                 FLUX_TRACE_POINT(10);
                 wg_ll_fetch<3>(ll + replica + LLLayout::kSwiglu, kInter, Contiguous{}, ep, wctx, vec);
                 __syncthreads();

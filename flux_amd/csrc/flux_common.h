@@ -122,26 +122,40 @@ __device__ __forceinline__ int slice1536_index(int lane, int j) {
     return 256 * (j >> 2) + 4 * lane + (j & 3);
 }
 
-// Weight rows are read once per token: non-temporal loads (the `nt` cache policy),
-// which measured 0.5% faster per decode token than default-policy loads, and 1.2%
-// together with non-temporal K/V copies.
+// Weight rows.  kStream selects non-temporal loads (the `nt` cache policy), which the
+// fused decode kernel uses (each row is read once per token: 0.5% faster per token, 1.2%
+// together with non-temporal K/V copies); the isolated kernels keep the default policy
+// (the gate/up kernel took 3.7 -> 7.0 us with non-temporal rows).
 typedef float f32x4_stream __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ f32x4_stream stream_load4(const float* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f32x4_stream*>(p));
+template <bool kStream>
+__device__ __forceinline__ float4 row_load4(const float* p) {
+    if constexpr (kStream) {
+        const f32x4_stream v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_stream*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const float4*>(p);
+    }
+}
+template <bool kStream>
+__device__ __forceinline__ float row_load1(const float* p) {
+    if constexpr (kStream) return __builtin_nontemporal_load(p);
+    else return *p;
 }
 
+template <bool kStream = false>
 __device__ __forceinline__ void load_row576(const float* __restrict__ row, int lane, float (&w)[9]) {
-    const f32x4_stream a = stream_load4(row + 4 * lane);
-    const f32x4_stream b = stream_load4(row + 256 + 4 * lane);
+    const float4 a = row_load4<kStream>(row + 4 * lane);
+    const float4 b = row_load4<kStream>(row + 256 + 4 * lane);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-    w[8] = __builtin_nontemporal_load(row + 512 + lane);
+    w[8] = row_load1<kStream>(row + 512 + lane);
 }
 
+template <bool kStream = false>
 __device__ __forceinline__ void load_row1536(const float* __restrict__ row, int lane, float (&w)[24]) {
 #pragma unroll
     for (int c = 0; c < 6; ++c) {
-        const f32x4_stream a = stream_load4(row + 256 * c + 4 * lane);
+        const float4 a = row_load4<kStream>(row + 256 * c + 4 * lane);
         w[4 * c + 0] = a.x; w[4 * c + 1] = a.y; w[4 * c + 2] = a.z; w[4 * c + 3] = a.w;
     }
 }
