@@ -406,6 +406,20 @@ __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_rea
 
 __device__ __forceinline__ int attn_k_index(int r, int d) { return r * kHeadDim + 4 * ((d >> 2) ^ (r & 15)) + (d & 3); }
 
+__device__ __forceinline__ uint32_t lds_address(const float* p) {
+    return static_cast<uint32_t>(reinterpret_cast<size_t>((__attribute__((address_space(3))) const float*)p));
+}
+
+// LDS-direct copies written as inline assembly, so that the compiler does not add a wait
+// for them (vmcnt(0)) before unrelated LDS reads; the wave that issues them reads the data
+// only after a later wait of its own (a poll's) has covered them.
+__device__ __forceinline__ void copy16_to_lds_nt(const float* src, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void copy4_to_lds_nt(const float* src, uint32_t lds) {
+    asm volatile("global_load_lds_dword %0, off nt" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
 // Copy rows [begin, begin + rows) of one KV head into the chunk's LDS layout.
 // One instruction moves 4 rows (1 KB): lane l -> row 4b + l/16, slot l%16.
 // Waves [first_wave, kWavesPerWG) issue the copies.
@@ -879,6 +893,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
     __shared__ float hvec[kHidden];   // layer input h (residual of C)
     __shared__ float rvec[kHidden];   // post-attention residual r (residual of E)
     __shared__ __align__(16) float vec[kInter];  // attention output / SwiGLU output / q of the group
+    __shared__ __align__(16) float oproj_rows[3][kHidden];  // this layer's o_proj rows of waves 0-2
     extern __shared__ __align__(16) float part[];  // K/V rows of the attention chunk; merge staging
 
     const int lane = tid_opaque() & 63;
@@ -973,6 +988,17 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     qkv_unit_compute(w, h, wn, Lw.eps, gw, lane, rp, key_layer + position * kHeadDim,
                                      value_layer + position * kHeadDim, head_stride, QkvLLOut{ll + LLLayout::kQkv, ep});
                 }
+            }
+
+            // The o_proj rows of phase C (waves 0-2) are copied into LDS now, during the
+            // attention, instead of after its merge.
+            if (wave_uniform(static_cast<int>(tid_opaque() >> 6)) < 3 && gw < kHidden) {
+                const int w3 = wave_uniform(static_cast<int>(tid_opaque() >> 6));
+                const float* row = Lw.o_proj + static_cast<int64_t>(gw) * kHidden;
+                const uint32_t dst = lds_address(oproj_rows[w3]);
+                copy16_to_lds_nt(row + 4 * lane, dst);
+                copy16_to_lds_nt(row + 256 + 4 * lane, dst + 1024);
+                copy4_to_lds_nt(row + 512 + lane, dst + 2048);
             }
 
             // ---- B: attention partial of (KV group g, position chunk c) ----
@@ -1079,13 +1105,12 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
             {
                 FLUX_TRACE_POINT(6);
                 const bool active = gw < kHidden;
-                float w[9];
-                if (active) load_row576<true>(Lw.o_proj + static_cast<int64_t>(gw) * kHidden, lane, w);
                 wg_ll_fetch<2>(ll + replica + LLLayout::kAttnMerged, kHidden, Contiguous{}, ep, wctx, vec);
-                __syncthreads();
+                __syncthreads();  // the poll's wait also covered this wave's o_proj row copy
                 FLUX_TRACE_POINT(7);
                 if (active) {
-                    float a[9];
+                    float w[9], a[9];
+                    lds_slice576(oproj_rows[wave_uniform(static_cast<int>(tid_opaque() >> 6)) % 3], lane, w);
                     lds_slice576(vec, lane, a);
                     const float dot = wave_sum_uniform(dot_lane<9>(a, w));
                     ll_store_replicas(ll + LLLayout::kResid, gw, hvec[gw] + dot, ep, lane);
