@@ -6,6 +6,9 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace flux {
 
@@ -32,6 +35,55 @@ hipError_t counted_free(void* ptr) {
     g_device_frees.fetch_add(1, std::memory_order_relaxed);
     return hipFree(ptr);
 }
+// Exchange arenas of the fused decode kernel live in uncached device memory
+// (hipDeviceMallocUncached): every access to them is a cross-CU publish or poll, and the
+// polls of an uncached arena return sooner (ctx 8192: 0.4368 against 0.4436 ms/token with
+// the arena in ordinary device memory).  Uncached memory that a kernel has read must not
+// be freed while the process runs (later allocations have then held wrong values on
+// MI355X), so arenas are never freed: a runtime takes one from this per-device pool and
+// gives it back when it is destroyed.  The runtime counts the take and the return as its
+// allocation and free; the pool holds at most as many arenas as runtimes were ever alive
+// at once on a device.
+class UncachedArenaPool {
+public:
+    hipError_t acquire(int device, size_t bytes, void** out) {
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            for (size_t i = 0; i < free_.size(); ++i) {
+                if (free_[i].device == device && free_[i].bytes == bytes) {
+                    *out = free_[i].ptr;
+                    free_[i] = free_.back();
+                    free_.pop_back();
+                    g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+                    return hipSuccess;
+                }
+            }
+        }
+        const hipError_t status = hipExtMallocWithFlags(out, bytes, hipDeviceMallocUncached);
+        if (status == hipSuccess) g_device_allocs.fetch_add(1, std::memory_order_relaxed);
+        return status;
+    }
+    void release(int device, size_t bytes, void* ptr) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        free_.push_back(Arena{device, bytes, ptr});
+        g_device_frees.fetch_add(1, std::memory_order_relaxed);
+    }
+
+private:
+    struct Arena {
+        int device;
+        size_t bytes;
+        void* ptr;
+    };
+    std::mutex mutex_;
+    std::vector<Arena> free_;
+};
+
+UncachedArenaPool& arena_pool() {
+    static UncachedArenaPool* pool = new UncachedArenaPool();  // never destroyed: the arenas outlive main
+    return *pool;
+}
+
 hipError_t counted_stream_sync(hipStream_t stream) {
     g_host_syncs.fetch_add(1, std::memory_order_relaxed);
     return hipStreamSynchronize(stream);
@@ -254,12 +306,14 @@ void DecodeRuntime::release() noexcept {
     }
     if (cache_block_) (void)counted_free(cache_block_);
     if (state_block_) (void)counted_free(state_block_);
+    if (ll_) arena_pool().release(device_, ll_bytes_, ll_);
     if (host_error_) (void)hipHostFree(host_error_);
     graph_exec_ = nullptr;
     graph_ = nullptr;
     completion_ = nullptr;
     capture_stream_ = nullptr;
     cache_block_ = state_block_ = nullptr;
+    ll_ = nullptr;
     host_error_ = host_error_device_ = nullptr;
     if (previous >= 0 && previous != device_) (void)hipSetDevice(previous);
 }
@@ -286,7 +340,6 @@ void DecodeRuntime::allocate() {
     const size_t o_counter = take(sizeof(uint32_t));
     const size_t o_error = take(sizeof(int32_t));
     const size_t o_layers = take(sizeof(LayerWeights) * kLayers);
-    const size_t o_ll = take(ll_bytes_);
     state_bytes_ = offset;
     check_hip(counted_malloc(&state_block_, state_bytes_), "allocating decode state");
     char* base = static_cast<char*>(state_block_);
@@ -299,7 +352,9 @@ void DecodeRuntime::allocate() {
     token_counter_ = reinterpret_cast<uint32_t*>(base + o_counter);
     error_ = reinterpret_cast<int32_t*>(base + o_error);
     layers_ = reinterpret_cast<LayerWeights*>(base + o_layers);
-    ll_ = reinterpret_cast<uint64_t*>(base + o_ll);
+    void* arena = nullptr;
+    check_hip(arena_pool().acquire(device_, ll_bytes_, &arena), "allocating the uncached exchange arena");
+    ll_ = static_cast<uint64_t*>(arena);
     // The kernel's error word also lands in mapped pinned host memory, so every runtime call
     // can see a finished launch's device error without synchronising.
     check_hip(hipHostMalloc(reinterpret_cast<void**>(&host_error_), sizeof(int32_t),
