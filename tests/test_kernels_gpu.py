@@ -315,13 +315,16 @@ def _attention_workspace(seq, device):
     return torch.empty(max(size.value // 4, 1), device=device)
 
 
-@pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (1024, 1024),
-                                          (1537, 1600), (2049, 2100), (3201, 3300), (4160, 4160)])
+@pytest.mark.parametrize("seq,capacity", [(1, 4), (63, 64), (64, 64), (65, 100), (200, 257), (300, 320),
+                                          (512, 600), (513, 513), (1024, 1024), (1537, 1600), (2049, 2100),
+                                          (3201, 3300), (4160, 4160)])
 def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
-    # Keys are split into chunks of 2 (up to 1024 tokens) to 16 (from about 4500 tokens on)
-    # 64-key tiles; from 129 tokens on some query tiles see several chunks and take the
-    # split-key path and its merge (1024: 2-tile chunks, eight of them, 3201: 10-tile chunks,
-    # six of them, and a one-query last tile).
+    # Up to 512 tokens one block per 32-query tile and head spreads the tile's 32-key chunks
+    # over 8 waves and combines them in LDS (300: some waves take two chunks, 512: every wave
+    # of the last tiles).  From 513 on, keys are split into chunks of 2 (up to 1024 tokens)
+    # to 16 (from about 4500 tokens on) 64-key tiles, and query tiles that see several
+    # chunks take the split-key path and its merge (1024: 2-tile chunks, eight of them,
+    # 3201: 10-tile chunks, six of them, and a one-query last tile).
     q = _randn(9, seq, D, seed=91).to(gpu_device)
     kc = _randn(3, capacity, D, seed=92).to(gpu_device)
     vc = _randn(3, capacity, D, seed=93).to(gpu_device)
@@ -337,7 +340,8 @@ def test_prefill_attention_matches_oracle(gpu_device, seq, capacity):
 @pytest.mark.parametrize("seq", [130, 16384])
 def test_prefill_attention_zero_query_prefix_mean(gpu_device, seq):
     # Zero queries make every visible key equally likely, so row s is the mean of V[0..s]:
-    # a closed form that pins the split-key merge at the largest capacity too.
+    # a closed form that pins the short-prompt kernel's in-block combine (130) and the
+    # split-key merge at the largest capacity (16384).
     capacity = seq
     q = torch.zeros(9, seq, D, device=gpu_device)
     kc = _randn(3, capacity, D, seed=94).to(gpu_device)
