@@ -116,7 +116,22 @@ struct GemmArgs {
     // where it can and otherwise runs the RMSNorm kernel first.
     const float* norm_weight;
     float norm_eps;
+    // Optional workspace that lets launch_gemm split K over kSplitBlocksK blocks when the
+    // split kernel's grid is small: kSplitBlocksK partial planes [M, N] followed by
+    // kSplitBlocksK partial row sums of squares [M] (folded norm), summed in order by a
+    // second kernel that applies the epilogue.  Null: every block covers all of K.
+    float* split_partials;
 };
+
+// Blocks that share one output tile's K range when GemmArgs::split_partials is given.
+constexpr int kSplitBlocksK = 3;
+// Prompt lengths up to which the prefill runtime provides the partial planes (longer
+// prompts fill the device without splitting K).
+constexpr int64_t kSplitKMaxRows = 1024;
+// Floats of GemmArgs::split_partials for an [M, N] GEMM.
+__host__ __device__ constexpr int64_t split_partials_floats(int64_t m, int64_t n) {
+    return kSplitBlocksK * m * n + kSplitBlocksK * m;
+}
 
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream);
 // epilogue(rmsnorm(A) * W^T): args.a holds the raw rows; `scratch` ([M, K]) receives the

@@ -432,7 +432,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // kStages = K / (kSplitWaves / RT * 16), fixed at compile time so the stage loop is
 // straight-line code and every wait names exactly the copies it needs.
-template <GemmEpilogue E, int kStages, int RT, bool kNorm, int kCols>
+// kKB > 1: blockIdx.x = column tile * kKB + kb, and block kb covers the kb-th third of K;
+// instead of the epilogue it writes its summed tile (and its rows' partial sums of squares)
+// to partial plane kb of args.split_partials for gemm_split_reduce_kernel.
+template <GemmEpilogue E, int kStages, int RT, bool kNorm, int kCols, int kKB>
 __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs args) {
     static_assert(kSplitStages == 5, "the buffers below are spelled out");
     static_assert(RT == 1 || RT == 2 || RT == 4, "row tiles per block");
@@ -460,10 +463,12 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     const int row_tile = wave % RT;
     const int part = wave / RT;
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32 * RT + 32 * row_tile;
-    const int n0 = blockIdx.x * kCols;
+    const int kb = kKB > 1 ? static_cast<int>(blockIdx.x % kKB) : 0;
+    const int n0 = static_cast<int>(blockIdx.x / kKB) * kCols;
     const int K = args.k;
-    constexpr int kSpan = kStages * kBK;  // this wave's K values start at part * kSpan
-    static_assert(!kNorm || kStages * kBK * kParts == kHidden, "the folded norm spans the hidden width");
+    constexpr int kSpan = kStages * kBK;  // this wave's K values start at (kb * kParts + part) * kSpan
+    const int k_first = (kb * kParts + part) * kSpan;
+    static_assert(!kNorm || kStages * kBK * kParts * kKB == kHidden, "the folded norm spans the hidden width");
     // Folded RMSNorm: the norm weights are requested before the first copies and stored to LDS
     // after them, so their latency overlaps the copies'.
     constexpr int kNormLoads = (kHidden + 64 * kSplitWaves - 1) / (64 * kSplitWaves);
@@ -489,7 +494,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         } else {
             base = args.b + static_cast<int64_t>(b_row<E>(n0 + row - 32, args.n)) * K;
         }
-        src[i] = base + part * kSpan + 4 * piece;
+        src[i] = base + k_first + 4 * piece;
     }
     auto slot = [&](auto bi) -> float* {
         constexpr int b = decltype(bi)::value % kSplitStages;
@@ -528,7 +533,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         o.a[1] = *reinterpret_cast<const f32x4*>(t + a_off1);
         if constexpr (kNorm) {
             // This lane's K values: pieces 2h and 2h + 1 of the stage.
-            const float* g = norm_g + part * kSpan + decltype(st)::value * kBK + 8 * h;
+            const float* g = norm_g + k_first + decltype(st)::value * kBK + 8 * h;
             o.g[0] = *reinterpret_cast<const f32x4*>(g);
             o.g[1] = *reinterpret_cast<const f32x4*>(g + 4);
         }
@@ -600,7 +605,54 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
         for (int p = 1; p < kParts; ++p) total += norm_ss[kNorm ? row_tile + RT * p : 0][row];
         return rms_inverse(total, kHidden, args.norm_eps);
     };
-    if constexpr (kParts == 1 && kCols == 32) {
+    if constexpr (kKB > 1) {
+        // Partial plane kb: this block's sums over its K range, unscaled; the norm's partial
+        // sums of squares per row go after the planes.
+        float* plane = args.split_partials + static_cast<int64_t>(kb) * args.m * args.n;
+        float* plane_ss = args.split_partials + static_cast<int64_t>(kKB) * args.m * args.n +
+                          static_cast<int64_t>(kb) * args.m;
+        if constexpr (kParts == 1) {
+#pragma unroll
+            for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t out_row = m0 + mfma32_row(lane, r);
+                    if (out_row < args.m) plane[out_row * args.n + n0 + 32 * j + (lane & 31)] = acc[j][r];
+                }
+            if constexpr (kNorm) {
+                if (lane < 32 && m0 + lane < args.m) plane_ss[m0 + lane] = norm_ss[row_tile][lane];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kTiles; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) partial[wave][j][r][lane] = acc[j][r];
+            __syncthreads();
+            const int j = lane & 31;
+#pragma unroll
+            for (int u = 0; u < 16 / kParts; ++u) {
+                const int r = (16 / kParts) * part + u;
+                float lo = partial[row_tile][0][r][lane], hi = partial[row_tile][kTiles - 1][r][lane];
+#pragma unroll
+                for (int p = 1; p < kParts; ++p) {
+                    lo += partial[row_tile + RT * p][0][r][lane];
+                    hi += partial[row_tile + RT * p][kTiles - 1][r][lane];
+                }
+                const int64_t out_row = m0 + mfma32_row(lane, r);
+                if (out_row >= args.m) continue;
+                plane[out_row * args.n + n0 + j] = lo;
+                if constexpr (kCols == 64) plane[out_row * args.n + n0 + 32 + j] = hi;
+            }
+            if constexpr (kNorm) {
+                if (part == 0 && lane < 32 && m0 + lane < args.m) {
+                    float total = norm_ss[row_tile][lane];
+#pragma unroll
+                    for (int p = 1; p < kParts; ++p) total += norm_ss[row_tile + RT * p][lane];
+                    plane_ss[m0 + lane] = total;
+                }
+            }
+        }
+    } else if constexpr (kParts == 1 && kCols == 32) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t out_row = m0 + mfma32_row(lane, r);
@@ -643,6 +695,50 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
             if constexpr (kCols == 64) gemm_store_pair<E>(args, out_row, n0, j, lo, hi);
             else gemm_store_one<E>(args, out_row, n0 + j, lo);
         }
+    }
+}
+
+// Sums the kSplitBlocksK partial planes of a K-split gemm_split_kernel in plane order and
+// applies the epilogue: thread -> (row, column pair j / j + 32 of a 64-column group) for
+// kCols = 64, (row, column) for kCols = 32.  The folded norm's row scale comes from the
+// summed partial sums of squares.
+template <GemmEpilogue E, bool kNorm, int kCols>
+__global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
+    constexpr bool kPair = kCols == 64;
+    const int units = kPair ? args.n / 2 : args.n;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= args.m * units) return;
+    const int64_t row = idx / units;
+    const int u = static_cast<int>(idx - row * units);
+    const int64_t plane = args.m * args.n;
+    const float* p = args.split_partials + row * args.n;
+    float inv = 1.0f;
+    if constexpr (kNorm) {
+        const float* ss = args.split_partials + kSplitBlocksK * plane + row;
+        float total = ss[0];
+#pragma unroll
+        for (int b = 1; b < kSplitBlocksK; ++b) total += ss[b * args.m];
+        inv = rms_inverse(total, kHidden, args.norm_eps);
+    }
+    if constexpr (kPair) {
+        const int g0 = (u >> 5) * 64;
+        const int j = u & 31;
+        float lo = p[g0 + j], hi = p[g0 + 32 + j];
+#pragma unroll
+        for (int b = 1; b < kSplitBlocksK; ++b) {
+            lo += p[b * plane + g0 + j];
+            hi += p[b * plane + g0 + 32 + j];
+        }
+        if constexpr (kNorm) {
+            lo *= inv;
+            hi *= inv;
+        }
+        gemm_store_pair<E>(args, row, g0, j, lo, hi);
+    } else {
+        float v = p[u];
+#pragma unroll
+        for (int b = 1; b < kSplitBlocksK; ++b) v += p[b * plane + u];
+        gemm_store_one<E>(args, row, u, v);
     }
 }
 
@@ -1352,6 +1448,7 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 // Grids below this many blocks (fewer than the device's CUs) use the ring kernel.
 constexpr int64_t kRingBlocks = 256;
 constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
+constexpr int64_t kSplitKBlocks = 256;  // ... and with K split over blocks while that grid fits it too
 
 // Tiling of gemm_split_kernel for this GEMM (rt = 0 when it does not take it), for K = 576
 // (hidden) or 1536 (intermediate), while the grid fits the device once.  Plain and residual
@@ -1389,12 +1486,23 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     if (norm && !split_folds_norm(args, epilogue)) return hipErrorInvalidValue;
     if (rt != 0) {
         const bool hidden = args.k == kHidden;
-        const dim3 grid(static_cast<unsigned>(args.n / shape.cols),
-                        static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
+        dim3 grid(static_cast<unsigned>(args.n / shape.cols), static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));
         const dim3 split_block(64 * kSplitWaves);
-#define FLUX_SPLIT_RT(E, ST, RT, NORM, COLS)                                                                          \
-    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT, NORM, COLS>), grid, split_block, 0, stream, \
-                       args)
+        // Grids of at most a third of the device split K over kSplitBlocksK blocks when the
+        // caller provides the partial planes.
+        const bool split_k = args.split_partials != nullptr &&
+                             static_cast<int64_t>(grid.x) * grid.y * kSplitBlocksK <= kSplitKBlocks;
+        if (split_k) grid.x *= kSplitBlocksK;
+#define FLUX_SPLIT_RT(E, ST, RT, NORM, COLS)                                                                        \
+    do {                                                                                                            \
+        if (split_k)                                                                                                \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT / kSplitBlocksK, RT, NORM, COLS,        \
+                                                                 kSplitBlocksK>),                                   \
+                               grid, split_block, 0, stream, args);                                                 \
+        else                                                                                                        \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_kernel<E, ST * RT, RT, NORM, COLS, 1>), grid, split_block, \
+                               0, stream, args);                                                                    \
+    } while (0)
 #define FLUX_LAUNCH_SPLIT(E)                                                                            \
     do {                                                                                                \
         if (rt == 1) {                                                                                  \
@@ -1439,6 +1547,31 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
 #undef FLUX_LAUNCH_SPLIT_NORM
 #undef FLUX_LAUNCH_SPLIT
 #undef FLUX_SPLIT_RT
+        hipError_t st = hipGetLastError();
+        if (st != hipSuccess || !split_k) return st;
+        const int64_t units = shape.cols == 64 ? args.n / 2 : args.n;
+        const dim3 rgrid(static_cast<unsigned>((args.m * units + 255) / 256));
+#define FLUX_REDUCE(E, NORM, COLS) \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<E, NORM, COLS>), rgrid, dim3(256), 0, stream, args)
+        switch (epilogue) {
+            case GemmEpilogue::kStore:
+                if (shape.cols == 32) FLUX_REDUCE(GemmEpilogue::kStore, false, 32);
+                else FLUX_REDUCE(GemmEpilogue::kStore, false, 64);
+                break;
+            case GemmEpilogue::kResidual:
+                if (shape.cols == 32) FLUX_REDUCE(GemmEpilogue::kResidual, false, 32);
+                else FLUX_REDUCE(GemmEpilogue::kResidual, false, 64);
+                break;
+            case GemmEpilogue::kSwiglu:
+                if (norm) FLUX_REDUCE(GemmEpilogue::kSwiglu, true, 64);
+                else FLUX_REDUCE(GemmEpilogue::kSwiglu, false, 64);
+                break;
+            case GemmEpilogue::kQkvRope:
+                if (norm) FLUX_REDUCE(GemmEpilogue::kQkvRope, true, 64);
+                else FLUX_REDUCE(GemmEpilogue::kQkvRope, false, 64);
+                break;
+        }
+#undef FLUX_REDUCE
         return hipGetLastError();
     }
     const dim3 block(kGemmThreads);

@@ -589,6 +589,10 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     const size_t o_attn = take(sizeof(float) * s * kHidden);
     const size_t o_swiglu = take(sizeof(float) * s * kInter);
     const size_t o_attn_ws = take(sizeof(float) * prefill_attention_workspace_floats(s));
+    // Partial planes of the K-split short-prompt GEMMs (their grids are small only for short
+    // prompts); sized for the widest GEMM, gate/up.
+    const bool split_k = s <= kSplitKMaxRows;
+    const size_t o_split = take(split_k ? sizeof(float) * split_partials_floats(s, kGateUp) : 0);
     const size_t o_final = take(sizeof(float) * kHidden);
     const size_t o_logits = take(sizeof(float) * vocab_);
     const size_t o_token = take(sizeof(int64_t));
@@ -607,6 +611,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     attn_rows_ = reinterpret_cast<float*>(base + o_attn);
     swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
     attn_workspace_ = reinterpret_cast<float*>(base + o_attn_ws);
+    split_partials_ = split_k ? reinterpret_cast<float*>(base + o_split) : nullptr;
     final_hidden_ = reinterpret_cast<float*>(base + o_final);
     logits_ = reinterpret_cast<float*>(base + o_logits);
     initial_token_ = reinterpret_cast<int64_t*>(base + o_token);
@@ -656,6 +661,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         float* keys = db.key_cache + layer * layer_elems;
         float* values = db.value_cache + layer * layer_elems;
         GemmArgs qkv{};
+        qkv.split_partials = split_partials_;
         qkv.a = hidden_a_;
         qkv.b = weights_.packed_qkv[layer];
         qkv.m = seq_;
@@ -673,6 +679,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
                                            attn_rows_, stream),
                   "launching prefill attention");
         GemmArgs o{};
+        o.split_partials = split_partials_;
         o.a = attn_rows_;
         o.b = weights_.o_proj[layer];
         o.c = hidden_b_;
@@ -682,6 +689,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         o.k = kHidden;
         check_hip(launch_gemm(o, GemmEpilogue::kResidual, stream), "launching o_proj GEMM");
         GemmArgs gu{};
+        gu.split_partials = split_partials_;
         gu.a = hidden_b_;
         gu.b = weights_.gate_up[layer];
         gu.c = swiglu_;
@@ -691,6 +699,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         check_hip(launch_norm_gemm(gu, weights_.post_norm[layer], eps_[layer], norm_, GemmEpilogue::kSwiglu, stream),
                   "launching post-attention RMSNorm + gate/up GEMM");
         GemmArgs dn{};
+        dn.split_partials = split_partials_;
         dn.a = swiglu_;
         dn.b = weights_.down[layer];
         dn.c = hidden_a_;

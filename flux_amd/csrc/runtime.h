@@ -153,6 +153,7 @@ private:
     float* query_ = nullptr;      // [9, S, 64]
     float* attn_rows_ = nullptr;  // [S, 576]
     float* attn_workspace_ = nullptr;  // split-key attention partials
+    float* split_partials_ = nullptr;  // K-split GEMM partial planes (short prompts), or null
     float* swiglu_ = nullptr;     // [S, 1536]
     float* final_hidden_ = nullptr;  // [576]
     float* logits_ = nullptr;     // [vocab]
