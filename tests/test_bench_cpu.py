@@ -17,7 +17,8 @@ def _fields() -> dict:
 
 
 def test_traffic_profile_matches_the_decode_source():
-    # None means the summary's sha256 is not the source's: re-run the counters after a kernel change.
+    # None means a sha256 in the summary is not its source's: re-run the counters after a change to the
+    # fused kernel or to the runtime that allocates its exchange arena.
     assert bench.profiled_traffic(128, 8192) is not None
 
 
