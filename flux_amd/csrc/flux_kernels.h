@@ -116,18 +116,21 @@ struct GemmArgs {
     // where it can and otherwise runs the RMSNorm kernel first.
     const float* norm_weight;
     float norm_eps;
-    // Optional workspace that lets launch_gemm split K over kSplitBlocksK blocks when the
-    // split kernel's grid is small: kSplitBlocksK partial planes [M, N] followed by
-    // kSplitBlocksK partial row sums of squares [M] (folded norm), summed in order by a
-    // second kernel that applies the epilogue.  Null: every block covers all of K.
+    // Optional workspace (split_partials_floats(M, N) floats) that lets launch_gemm split K
+    // over kSplitBlocksK blocks when the split kernel's or the 576-column kernel's grid is
+    // small: kSplitBlocksK partial planes [M, N] followed by kSplitBlocksK partial row sums
+    // of squares [M] (folded norm), summed in order by a second kernel that applies the
+    // epilogue.  Null: every block covers all of K.
     float* split_partials;
 };
 
 // Blocks that share one output tile's K range when GemmArgs::split_partials is given.
 constexpr int kSplitBlocksK = 3;
 // Prompt lengths up to which the prefill runtime provides the partial planes (longer
-// prompts fill the device without splitting K).
+// prompts fill the device without splitting K): for the widest GEMM (gate/up) up to
+// kSplitKMaxRows rows, for the 576-column GEMMs up to kNarrowSplitMaxRows.
 constexpr int64_t kSplitKMaxRows = 1024;
+constexpr int64_t kNarrowSplitMaxRows = 4096;
 // Floats of GemmArgs::split_partials for an [M, N] GEMM.
 __host__ __device__ constexpr int64_t split_partials_floats(int64_t m, int64_t n) {
     return kSplitBlocksK * m * n + kSplitBlocksK * m;

@@ -702,7 +702,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
 // applies the epilogue: thread -> (row, column pair j / j + 32 of a 64-column group) for
 // kCols = 64, (row, column) for kCols = 32.  The folded norm's row scale comes from the
 // summed partial sums of squares.
-template <GemmEpilogue E, bool kNorm, int kCols>
+template <GemmEpilogue E, bool kNorm, int kCols, int kPlanes = kSplitBlocksK>
 __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
     constexpr bool kPair = kCols == 64;
     const int units = kPair ? args.n / 2 : args.n;
@@ -714,10 +714,10 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
     const float* p = args.split_partials + row * args.n;
     float inv = 1.0f;
     if constexpr (kNorm) {
-        const float* ss = args.split_partials + kSplitBlocksK * plane + row;
+        const float* ss = args.split_partials + kPlanes * plane + row;
         float total = ss[0];
 #pragma unroll
-        for (int b = 1; b < kSplitBlocksK; ++b) total += ss[b * args.m];
+        for (int b = 1; b < kPlanes; ++b) total += ss[b * args.m];
         inv = rms_inverse(total, kHidden, args.norm_eps);
     }
     if constexpr (kPair) {
@@ -725,7 +725,7 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
         const int j = u & 31;
         float lo = p[g0 + j], hi = p[g0 + 32 + j];
 #pragma unroll
-        for (int b = 1; b < kSplitBlocksK; ++b) {
+        for (int b = 1; b < kPlanes; ++b) {
             lo += p[b * plane + g0 + j];
             hi += p[b * plane + g0 + 32 + j];
         }
@@ -737,7 +737,7 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
     } else {
         float v = p[u];
 #pragma unroll
-        for (int b = 1; b < kSplitBlocksK; ++b) v += p[b * plane + u];
+        for (int b = 1; b < kPlanes; ++b) v += p[b * plane + u];
         gemm_store_one<E>(args, row, u, v);
     }
 }
@@ -751,7 +751,10 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
 // with three copies in flight, stepped as in gemm_ring_kernel.  For every grid size:
 // at 8192 rows the ring measured 0.3 ms per prefill faster than two buffers (which
 // fit more blocks per CU but wait on each stage's copy).
-template <GemmEpilogue E>
+// kKB > 1: blockIdx.x = column tile * kKB + kb; block kb covers the kb-th part of K and
+// writes its tile to partial plane kb of args.split_partials (gemm_split_reduce_kernel sums
+// the planes and applies the epilogue).
+template <GemmEpilogue E, int kKB>
 __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args) {
     static_assert(E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual, "plain epilogues only");
     constexpr int kNS = 4;
@@ -772,8 +775,10 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
     const int wm = wave >> 1;
     const int wn = wave & 1;
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kRows;
-    const int n0 = blockIdx.x * kRows;
+    const int kb = kKB > 1 ? static_cast<int>(blockIdx.x % kKB) : 0;
+    const int n0 = static_cast<int>(blockIdx.x / kKB) * kRows;
     const int K = args.k;
+    const int k_first = kb * (K / kKB);
 
     const float* a_src[2];
     const float* b_src[2];
@@ -782,8 +787,8 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
         const int row = 8 * (wave + 4 * j) + (lane >> 3);
         const int piece = (lane & 7) ^ ((row >> 1) & 7);
         const int64_t ga = m0 + row < args.m ? m0 + row : args.m - 1;
-        a_src[j] = args.a + ga * K + 4 * piece;
-        b_src[j] = args.b + static_cast<int64_t>(n0 + row) * K + 4 * piece;
+        a_src[j] = args.a + ga * K + k_first + 4 * piece;
+        b_src[j] = args.b + static_cast<int64_t>(n0 + row) * K + k_first + 4 * piece;
     }
     auto abuf = [&](auto bi) -> float* {
         constexpr int b = decltype(bi)::value;
@@ -799,7 +804,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
         else if constexpr (b == 2) return b_s2;
         else return b_s3;
     };
-    const int stages = K / kDepth;
+    const int stages = K / kKB / kDepth;
     auto issue = [&](auto bi, int st) {
         const int k0 = (st < stages ? st : stages - 1) * kDepth;
         float* as = abuf(bi);
@@ -860,12 +865,15 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
     wait_vmcnt<0>();  // no copy may still be landing in LDS when the block retires
 
     const int col = n0 + wn * 32 + (lane & 31);
+    float* plane = args.split_partials + static_cast<int64_t>(kb) * args.m * args.n;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * 32 + mfma32_row(lane, r);
         if (row >= args.m) continue;
         const int64_t i0 = row * args.n + col;
-        if constexpr (E == GemmEpilogue::kResidual) {
+        if constexpr (kKB > 1) {
+            plane[i0] = acc[r];
+        } else if constexpr (E == GemmEpilogue::kResidual) {
             args.c[i0] = args.residual[i0] + acc[r];
         } else {
             args.c[i0] = acc[r];
@@ -1449,6 +1457,7 @@ __global__ void embedding_gather_kernel(const int64_t* ids, const float* embeddi
 constexpr int64_t kRingBlocks = 256;
 constexpr int64_t kSplitBlocks = 256;  // gemm_split_kernel while its grid fits the device once
 constexpr int64_t kSplitKBlocks = 256;  // ... and with K split over blocks while that grid fits it too
+constexpr int64_t kNarrowSplitBlocks = 1024;  // gemm_narrow_kernel splits K while the split grid is at most 4 per CU
 
 // Tiling of gemm_split_kernel for this GEMM (rt = 0 when it does not take it), for K = 576
 // (hidden) or 1536 (intermediate), while the grid fits the device once.  Plain and residual
@@ -1577,13 +1586,32 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     const dim3 block(kGemmThreads);
     if ((epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) && args.n % kBN != 0 &&
         args.k % 32 == 0) {
-        // Column counts that are not a multiple of 128 (576): 64 x 64 tiles.
-        const dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
+        // Column counts that are not a multiple of 128 (576): 64 x 64 tiles.  Grids that leave
+        // CUs idle split K over kSplitBlocksK blocks per tile when the caller provides the
+        // partial planes.
+        dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
+        const bool split_k = args.split_partials != nullptr && args.k % (32 * kSplitBlocksK) == 0 &&
+                             static_cast<int64_t>(grid.x) * grid.y * kSplitBlocksK <= kNarrowSplitBlocks;
+        if (split_k) grid.x *= kSplitBlocksK;
+#define FLUX_NARROW(E)                                                                                             \
+    do {                                                                                                           \
+        if (split_k)                                                                                               \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, kSplitBlocksK>), grid, block, 0, stream, args); \
+        else                                                                                                       \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 1>), grid, block, 0, stream, args);            \
+    } while (0)
+        if (epilogue == GemmEpilogue::kResidual) FLUX_NARROW(GemmEpilogue::kResidual);
+        else FLUX_NARROW(GemmEpilogue::kStore);
+#undef FLUX_NARROW
+        hipError_t st = hipGetLastError();
+        if (st != hipSuccess || !split_k) return st;
+        const dim3 rgrid(static_cast<unsigned>((args.m * args.n + 255) / 256));
         if (epilogue == GemmEpilogue::kResidual)
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kResidual>), grid, block, 0, stream,
-                               args);
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32>), rgrid,
+                               dim3(256), 0, stream, args);
         else
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<GemmEpilogue::kStore>), grid, block, 0, stream, args);
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kStore, false, 32>), rgrid,
+                               dim3(256), 0, stream, args);
         return hipGetLastError();
     }
     // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles;

@@ -589,10 +589,11 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     const size_t o_attn = take(sizeof(float) * s * kHidden);
     const size_t o_swiglu = take(sizeof(float) * s * kInter);
     const size_t o_attn_ws = take(sizeof(float) * prefill_attention_workspace_floats(s));
-    // Partial planes of the K-split short-prompt GEMMs (their grids are small only for short
-    // prompts); sized for the widest GEMM, gate/up.
-    const bool split_k = s <= kSplitKMaxRows;
-    const size_t o_split = take(split_k ? sizeof(float) * split_partials_floats(s, kGateUp) : 0);
+    // Partial planes of the K-split GEMMs, whose grids are small only for short and mid-length
+    // prompts: sized for gate/up up to kSplitKMaxRows rows, for the 576-column GEMMs beyond.
+    const bool split_k = s <= kNarrowSplitMaxRows;
+    const int64_t split_n = s <= kSplitKMaxRows ? kGateUp : kHidden;
+    const size_t o_split = take(split_k ? sizeof(float) * split_partials_floats(s, split_n) : 0);
     const size_t o_final = take(sizeof(float) * kHidden);
     const size_t o_logits = take(sizeof(float) * vocab_);
     const size_t o_token = take(sizeof(int64_t));
