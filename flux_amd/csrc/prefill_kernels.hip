@@ -1590,13 +1590,22 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         // CUs idle split K over kSplitBlocksK blocks per tile when the caller provides the
         // partial planes.
         dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
+        const int64_t blocks = static_cast<int64_t>(grid.x) * grid.y;
         const bool split_k = args.split_partials != nullptr && args.k % (32 * kSplitBlocksK) == 0 &&
-                             static_cast<int64_t>(grid.x) * grid.y * kSplitBlocksK <= kNarrowSplitBlocks;
+                             blocks * kSplitBlocksK <= kNarrowSplitBlocks;
+        // Beyond that, two K halves when they cut the blocks the busiest CU runs (in units of
+        // a whole-K block) by at least 15%: ceil(2B / 256) / 2 against ceil(B / 256).
+        const int64_t cus = 256;
+        const bool split2 = !split_k && args.split_partials != nullptr && args.k % 64 == 0 &&
+                            20 * ((2 * blocks + cus - 1) / cus) <= 17 * 2 * ((blocks + cus - 1) / cus);
         if (split_k) grid.x *= kSplitBlocksK;
+        if (split2) grid.x *= 2;
 #define FLUX_NARROW(E)                                                                                             \
     do {                                                                                                           \
         if (split_k)                                                                                               \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, kSplitBlocksK>), grid, block, 0, stream, args); \
+        else if (split2)                                                                                           \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 2>), grid, block, 0, stream, args);            \
         else                                                                                                       \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 1>), grid, block, 0, stream, args);            \
     } while (0)
@@ -1604,8 +1613,17 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         else FLUX_NARROW(GemmEpilogue::kStore);
 #undef FLUX_NARROW
         hipError_t st = hipGetLastError();
-        if (st != hipSuccess || !split_k) return st;
+        if (st != hipSuccess || !(split_k || split2)) return st;
         const dim3 rgrid(static_cast<unsigned>((args.m * args.n + 255) / 256));
+        if (split2) {
+            if (epilogue == GemmEpilogue::kResidual)
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32, 2>),
+                                   rgrid, dim3(256), 0, stream, args);
+            else
+                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kStore, false, 32, 2>),
+                                   rgrid, dim3(256), 0, stream, args);
+            return hipGetLastError();
+        }
         if (epilogue == GemmEpilogue::kResidual)
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32>), rgrid,
                                dim3(256), 0, stream, args);
