@@ -117,9 +117,9 @@ struct GemmArgs {
     const float* norm_weight;
     float norm_eps;
     // Optional workspace (split_partials_floats(M, N) floats) that lets launch_gemm split K
-    // over kSplitBlocksK blocks when the split kernel's or the 576-column kernel's grid is
-    // small: kSplitBlocksK partial planes [M, N] followed by kSplitBlocksK partial row sums
-    // of squares [M] (folded norm), summed in order by a second kernel that applies the
+    // over kSplitBlocksK (or, for the 576-column kernel, two) blocks when the grid leaves CUs
+    // idle: one partial plane [M, N] per K part, then kSplitBlocksK partial row sums of
+    // squares [M] (folded norm), summed in order by a second kernel that applies the
     // epilogue.  Null: every block covers all of K.
     float* split_partials;
 };
