@@ -130,7 +130,7 @@ constexpr int kSplitBlocksK = 3;
 // prompts fill the device without splitting K): for the widest GEMM (gate/up) up to
 // kSplitKMaxRows rows, for the 576-column GEMMs up to kNarrowSplitMaxRows.
 constexpr int64_t kSplitKMaxRows = 1024;
-constexpr int64_t kNarrowSplitMaxRows = 4096;
+constexpr int64_t kNarrowSplitMaxRows = 16384;
 // Floats of GemmArgs::split_partials for an [M, N] GEMM.
 __host__ __device__ constexpr int64_t split_partials_floats(int64_t m, int64_t n) {
     return kSplitBlocksK * m * n + kSplitBlocksK * m;
@@ -141,6 +141,13 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
 // normalized rows when the norm cannot be folded into the GEMM.
 hipError_t launch_norm_gemm(const GemmArgs& args, const float* norm_weight, float eps, float* scratch,
                             GemmEpilogue epilogue, hipStream_t stream);
+// True when launch_norm_gemm folds the RMSNorm into this GEMM (no separate norm launch).
+bool gemm_folds_norm(const GemmArgs& args, GemmEpilogue epilogue);
+// c = residual + A·Wᵀ (args with the residual epilogue) and norm_out = rmsnorm(c) with the
+// given weights: the norm that the next GEMM needs when it does not fold it.  A K-split
+// 576-column GEMM reduces its partial planes inside the norm kernel.
+hipError_t launch_gemm_residual_norm(const GemmArgs& args, const float* norm_weight, float eps, float* norm_out,
+                                     hipStream_t stream);
 
 // Workspace (floats) of launch_prefill_attention for a prompt of `seq` tokens (0 when
 // every query tile fits in one key chunk).

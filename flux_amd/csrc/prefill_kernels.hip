@@ -742,6 +742,55 @@ __global__ void __launch_bounds__(256) gemm_split_reduce_kernel(GemmArgs args) {
     }
 }
 
+// The reduce of a K-split 576-column GEMM with the residual epilogue, folded into the RMSNorm
+// of its output: c = residual + (plane 0 + plane 1 + ...) and norm_out = w * (c * inv_rms(c)).
+// Wave per row, the row in registers as float4 quads; the sums run in the order of
+// gemm_split_reduce_kernel and the norm in that of rmsnorm_wave4_kernel, so both outputs are
+// bitwise those of the reduce kernel followed by launch_rmsnorm_rows.
+template <int kPlanes>
+__global__ void __launch_bounds__(256) split_reduce_residual_norm_kernel(GemmArgs args, const float* __restrict__ w,
+                                                                         float eps, float* __restrict__ norm_out) {
+    constexpr int kQuads = 3;  // 144 quads of a 576-wide row over 64 lanes
+    const int lane = threadIdx.x & 63;
+    const int64_t plane = args.m * kHidden;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < args.m;
+         row += static_cast<int64_t>(gridDim.x) * 4) {
+        float4 v[kQuads];
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c < kHidden) {
+                const float* p = args.split_partials + row * kHidden + c;
+                float4 a = *reinterpret_cast<const float4*>(p);
+#pragma unroll
+                for (int b = 1; b < kPlanes; ++b) {
+                    const float4 q = *reinterpret_cast<const float4*>(p + b * plane);
+                    a = make_float4(a.x + q.x, a.y + q.y, a.z + q.z, a.w + q.w);
+                }
+                const float4 r = *reinterpret_cast<const float4*>(args.residual + row * kHidden + c);
+                v[j] = make_float4(r.x + a.x, r.y + a.y, r.z + a.z, r.w + a.w);
+                *reinterpret_cast<float4*>(args.c + row * kHidden + c) = v[j];
+                ss = fmaf(v[j].x, v[j].x, ss);
+                ss = fmaf(v[j].y, v[j].y, ss);
+                ss = fmaf(v[j].z, v[j].z, ss);
+                ss = fmaf(v[j].w, v[j].w, ss);
+            }
+        }
+        const float inv = rms_inverse(wave_sum(ss), kHidden, eps);
+#pragma unroll
+        for (int j = 0; j < kQuads; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c < kHidden) {
+                const float4 g = *reinterpret_cast<const float4*>(w + c);
+                *reinterpret_cast<float4*>(norm_out + row * kHidden + c) =
+                    make_float4(g.x * (v[j].x * inv), g.y * (v[j].y * inv), g.z * (v[j].z * inv),
+                                g.w * (v[j].w * inv));
+            }
+        }
+    }
+}
+
 // Narrow-column GEMM for the residual / plain epilogues of N = 576 outputs (o_proj,
 // down): block tile 64 x 64, 4 waves in 2 x 2, wave tile 32 x 32 (one accumulator
 // chain).  576 columns are 9 such tiles, so no wave computes a padded column group,
@@ -1485,6 +1534,45 @@ static bool split_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) {
            split_shape(args, epilogue).rt != 0;
 }
 
+// K parts of the 576-column kernel: kSplitBlocksK while that grid is at most
+// kNarrowSplitBlocks blocks; beyond that two halves when they cut the blocks the busiest CU
+// runs (in units of a whole-K block: ceil(2B / 256) / 2 against ceil(B / 256), B blocks) by
+// at least 15%, or by at least 5% when the reduce is folded into the RMSNorm that follows
+// (launch_gemm_residual_norm).  1 without partial planes.
+static int narrow_parts(const GemmArgs& args, bool fused_reduce) {
+    if (args.split_partials == nullptr) return 1;
+    const int64_t blocks = static_cast<int64_t>(args.n / 64) * ((args.m + 63) / 64);
+    if (args.k % (32 * kSplitBlocksK) == 0 && blocks * kSplitBlocksK <= kNarrowSplitBlocks) return kSplitBlocksK;
+    const int64_t cus = 256;
+    const int64_t whole = (blocks + cus - 1) / cus;
+    const int64_t halves = (2 * blocks + cus - 1) / cus;
+    const int64_t keep = fused_reduce ? 19 : 17;  // per 20: the half-block count must stay under keep/20
+    return args.k % 64 == 0 && 20 * halves <= keep * 2 * whole ? 2 : 1;
+}
+
+static hipError_t launch_narrow(const GemmArgs& args, GemmEpilogue epilogue, int parts, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(args.n / 64 * parts), static_cast<unsigned>((args.m + 63) / 64));
+    const dim3 block(kGemmThreads);
+#define FLUX_NARROW(E)                                                                                             \
+    do {                                                                                                           \
+        if (parts == kSplitBlocksK)                                                                                \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, kSplitBlocksK>), grid, block, 0, stream, args); \
+        else if (parts == 2)                                                                                       \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 2>), grid, block, 0, stream, args);            \
+        else                                                                                                       \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 1>), grid, block, 0, stream, args);            \
+    } while (0)
+    if (epilogue == GemmEpilogue::kResidual) FLUX_NARROW(GemmEpilogue::kResidual);
+    else FLUX_NARROW(GemmEpilogue::kStore);
+#undef FLUX_NARROW
+    return hipGetLastError();
+}
+
+static bool narrow_shape(const GemmArgs& args, GemmEpilogue epilogue) {
+    return (epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) && args.n % kBN != 0 &&
+           args.k % 32 == 0;
+}
+
 hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
@@ -1584,52 +1672,25 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         return hipGetLastError();
     }
     const dim3 block(kGemmThreads);
-    if ((epilogue == GemmEpilogue::kStore || epilogue == GemmEpilogue::kResidual) && args.n % kBN != 0 &&
-        args.k % 32 == 0) {
-        // Column counts that are not a multiple of 128 (576): 64 x 64 tiles.  Grids that leave
-        // CUs idle split K over kSplitBlocksK blocks per tile when the caller provides the
-        // partial planes.
-        dim3 grid(static_cast<unsigned>(args.n / 64), static_cast<unsigned>((args.m + 63) / 64));
-        const int64_t blocks = static_cast<int64_t>(grid.x) * grid.y;
-        const bool split_k = args.split_partials != nullptr && args.k % (32 * kSplitBlocksK) == 0 &&
-                             blocks * kSplitBlocksK <= kNarrowSplitBlocks;
-        // Beyond that, two K halves when they cut the blocks the busiest CU runs (in units of
-        // a whole-K block) by at least 15%: ceil(2B / 256) / 2 against ceil(B / 256).
-        const int64_t cus = 256;
-        const bool split2 = !split_k && args.split_partials != nullptr && args.k % 64 == 0 &&
-                            20 * ((2 * blocks + cus - 1) / cus) <= 17 * 2 * ((blocks + cus - 1) / cus);
-        if (split_k) grid.x *= kSplitBlocksK;
-        if (split2) grid.x *= 2;
-#define FLUX_NARROW(E)                                                                                             \
-    do {                                                                                                           \
-        if (split_k)                                                                                               \
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, kSplitBlocksK>), grid, block, 0, stream, args); \
-        else if (split2)                                                                                           \
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 2>), grid, block, 0, stream, args);            \
-        else                                                                                                       \
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_narrow_kernel<E, 1>), grid, block, 0, stream, args);            \
-    } while (0)
-        if (epilogue == GemmEpilogue::kResidual) FLUX_NARROW(GemmEpilogue::kResidual);
-        else FLUX_NARROW(GemmEpilogue::kStore);
-#undef FLUX_NARROW
-        hipError_t st = hipGetLastError();
-        if (st != hipSuccess || !(split_k || split2)) return st;
+    if (narrow_shape(args, epilogue)) {
+        // Column counts that are not a multiple of 128 (576): 64 x 64 tiles, K split over
+        // blocks where the grid leaves CUs idle (narrow_parts).
+        const int parts = narrow_parts(args, false);
+        hipError_t st = launch_narrow(args, epilogue, parts, stream);
+        if (st != hipSuccess || parts == 1) return st;
         const dim3 rgrid(static_cast<unsigned>((args.m * args.n + 255) / 256));
-        if (split2) {
-            if (epilogue == GemmEpilogue::kResidual)
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32, 2>),
-                                   rgrid, dim3(256), 0, stream, args);
-            else
-                hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kStore, false, 32, 2>),
-                                   rgrid, dim3(256), 0, stream, args);
-            return hipGetLastError();
-        }
-        if (epilogue == GemmEpilogue::kResidual)
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32>), rgrid,
-                               dim3(256), 0, stream, args);
-        else
-            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kStore, false, 32>), rgrid,
-                               dim3(256), 0, stream, args);
+#define FLUX_REDUCE_PLAIN(P)                                                                                        \
+    do {                                                                                                            \
+        if (epilogue == GemmEpilogue::kResidual)                                                                    \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kResidual, false, 32, P>),    \
+                               rgrid, dim3(256), 0, stream, args);                                                  \
+        else                                                                                                        \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_split_reduce_kernel<GemmEpilogue::kStore, false, 32, P>), rgrid, \
+                               dim3(256), 0, stream, args);                                                         \
+    } while (0)
+        if (parts == 2) FLUX_REDUCE_PLAIN(2);
+        else FLUX_REDUCE_PLAIN(kSplitBlocksK);
+#undef FLUX_REDUCE_PLAIN
         return hipGetLastError();
     }
     // 128-row tiles when they already give the device two blocks per CU, else 64-row tiles;
@@ -1679,6 +1740,30 @@ hipError_t launch_norm_gemm(const GemmArgs& args, const float* norm_weight, floa
     plain.a = scratch;
     plain.norm_weight = nullptr;
     return launch_gemm(plain, epilogue, stream);
+}
+
+bool gemm_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) { return split_folds_norm(args, epilogue); }
+
+hipError_t launch_gemm_residual_norm(const GemmArgs& args, const float* norm_weight, float eps, float* norm_out,
+                                     hipStream_t stream) {
+    const int parts = narrow_shape(args, GemmEpilogue::kResidual) && args.n == kHidden && split_shape(args, GemmEpilogue::kResidual).rt == 0
+                          ? narrow_parts(args, true)
+                          : 1;
+    if (parts == 1) {
+        const hipError_t e = launch_gemm(args, GemmEpilogue::kResidual, stream);
+        if (e != hipSuccess) return e;
+        return launch_rmsnorm_rows(args.c, norm_weight, norm_out, args.m, static_cast<int>(args.n), eps, stream);
+    }
+    const hipError_t e = launch_narrow(args, GemmEpilogue::kResidual, parts, stream);
+    if (e != hipSuccess) return e;
+    const int64_t grid = (args.m + 3) / 4 < 65535 ? (args.m + 3) / 4 : 65535;
+    if (parts == 2)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(split_reduce_residual_norm_kernel<2>), dim3(static_cast<unsigned>(grid)),
+                           dim3(256), 0, stream, args, norm_weight, eps, norm_out);
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(split_reduce_residual_norm_kernel<kSplitBlocksK>),
+                           dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream, args, norm_weight, eps, norm_out);
+    return hipGetLastError();
 }
 
 size_t prefill_attention_workspace_floats(int64_t seq) {

@@ -658,12 +658,24 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
     check_hip(launch_embedding_gather(input_ids, weights_.embedding, vocab_, seq_, hidden_a_, stream),
               "launching embedding gather");
     const int64_t layer_elems = static_cast<int64_t>(kKVHeads) * capacity_ * kHeadDim;
+    // The QKV and gate/up GEMMs fold their RMSNorm for short prompts; otherwise the norm runs
+    // with the o_proj / down GEMM before it (launch_gemm_residual_norm), which lets a K-split
+    // GEMM reduce its partial planes inside the norm kernel.
+    GemmArgs qkv_shape{};
+    qkv_shape.m = seq_;
+    qkv_shape.n = kQKV;
+    qkv_shape.k = kHidden;
+    GemmArgs gu_shape{};
+    gu_shape.m = seq_;
+    gu_shape.n = kGateUp;
+    gu_shape.k = kHidden;
+    const bool qkv_folds = gemm_folds_norm(qkv_shape, GemmEpilogue::kQkvRope);
+    const bool gu_folds = gemm_folds_norm(gu_shape, GemmEpilogue::kSwiglu);
     for (int layer = 0; layer < kLayers; ++layer) {
         float* keys = db.key_cache + layer * layer_elems;
         float* values = db.value_cache + layer * layer_elems;
         GemmArgs qkv{};
         qkv.split_partials = split_partials_;
-        qkv.a = hidden_a_;
         qkv.b = weights_.packed_qkv[layer];
         qkv.m = seq_;
         qkv.n = kQKV;
@@ -674,8 +686,15 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         qkv.key_cache = keys;
         qkv.value_cache = values;
         qkv.capacity = capacity_;
-        check_hip(launch_norm_gemm(qkv, weights_.input_norm[layer], eps_[layer], norm_, GemmEpilogue::kQkvRope, stream),
-                  "launching input RMSNorm + QKV GEMM");
+        if (layer == 0 || qkv_folds) {
+            qkv.a = hidden_a_;
+            check_hip(launch_norm_gemm(qkv, weights_.input_norm[layer], eps_[layer], norm_, GemmEpilogue::kQkvRope,
+                                       stream),
+                      "launching input RMSNorm + QKV GEMM");
+        } else {
+            qkv.a = norm_;  // normalized by the previous layer's down GEMM + norm
+            check_hip(launch_gemm(qkv, GemmEpilogue::kQkvRope, stream), "launching QKV GEMM");
+        }
         check_hip(launch_prefill_attention(query_, keys, values, seq_, capacity_, scales_[layer], attn_workspace_,
                                            attn_rows_, stream),
                   "launching prefill attention");
@@ -688,17 +707,24 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         o.m = seq_;
         o.n = kHidden;
         o.k = kHidden;
-        check_hip(launch_gemm(o, GemmEpilogue::kResidual, stream), "launching o_proj GEMM");
         GemmArgs gu{};
         gu.split_partials = split_partials_;
-        gu.a = hidden_b_;
         gu.b = weights_.gate_up[layer];
         gu.c = swiglu_;
         gu.m = seq_;
         gu.n = kGateUp;
         gu.k = kHidden;
-        check_hip(launch_norm_gemm(gu, weights_.post_norm[layer], eps_[layer], norm_, GemmEpilogue::kSwiglu, stream),
-                  "launching post-attention RMSNorm + gate/up GEMM");
+        if (gu_folds) {
+            check_hip(launch_gemm(o, GemmEpilogue::kResidual, stream), "launching o_proj GEMM");
+            gu.a = hidden_b_;
+            check_hip(launch_norm_gemm(gu, weights_.post_norm[layer], eps_[layer], norm_, GemmEpilogue::kSwiglu, stream),
+                      "launching post-attention RMSNorm + gate/up GEMM");
+        } else {
+            check_hip(launch_gemm_residual_norm(o, weights_.post_norm[layer], eps_[layer], norm_, stream),
+                      "launching o_proj GEMM + post-attention RMSNorm");
+            gu.a = norm_;
+            check_hip(launch_gemm(gu, GemmEpilogue::kSwiglu, stream), "launching gate/up GEMM");
+        }
         GemmArgs dn{};
         dn.split_partials = split_partials_;
         dn.a = swiglu_;
@@ -708,7 +734,12 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         dn.m = seq_;
         dn.n = kHidden;
         dn.k = kInter;
-        check_hip(launch_gemm(dn, GemmEpilogue::kResidual, stream), "launching down GEMM");
+        if (layer + 1 < kLayers && !qkv_folds) {
+            check_hip(launch_gemm_residual_norm(dn, weights_.input_norm[layer + 1], eps_[layer + 1], norm_, stream),
+                      "launching down GEMM + next input RMSNorm");
+        } else {
+            check_hip(launch_gemm(dn, GemmEpilogue::kResidual, stream), "launching down GEMM");
+        }
     }
     const float* last_row = hidden_a_ + (seq_ - 1) * kHidden;
     check_hip(launch_rmsnorm_rows(last_row, weights_.final_norm, final_hidden_, 1, kHidden, eps_[0], stream),
