@@ -1746,9 +1746,14 @@ bool gemm_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) { return split
 
 hipError_t launch_gemm_residual_norm(const GemmArgs& args, const float* norm_weight, float eps, float* norm_out,
                                      hipStream_t stream) {
-    const int parts = narrow_shape(args, GemmEpilogue::kResidual) && args.n == kHidden && split_shape(args, GemmEpilogue::kResidual).rt == 0
-                          ? narrow_parts(args, true)
-                          : 1;
+    // The fused kernel reads and writes rows as float4: every buffer must be 16-byte aligned
+    // (a norm weight that is a view into a larger tensor may not be), else the plain path runs.
+    auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool fusable = narrow_shape(args, GemmEpilogue::kResidual) && args.n == kHidden &&
+                         split_shape(args, GemmEpilogue::kResidual).rt == 0 && aligned(args.c) &&
+                         aligned(args.residual) && aligned(args.split_partials) && aligned(norm_weight) &&
+                         aligned(norm_out);
+    const int parts = fusable ? narrow_parts(args, true) : 1;
     if (parts == 1) {
         const hipError_t e = launch_gemm(args, GemmEpilogue::kResidual, stream);
         if (e != hipSuccess) return e;
