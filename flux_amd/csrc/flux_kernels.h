@@ -122,6 +122,7 @@ struct GemmArgs {
     // squares [M] (folded norm), summed in order by a second kernel that applies the
     // epilogue.  Null: every block covers all of K.
     float* split_partials;
+    int64_t split_floats;  // floats available at split_partials: no split whose planes exceed it
 };
 
 // Blocks that share one output tile's K range when GemmArgs::split_partials is given.

@@ -1539,10 +1539,18 @@ static bool split_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) {
 // runs (in units of a whole-K block: ceil(2B / 256) / 2 against ceil(B / 256), B blocks) by
 // at least 15%, or by at least 5% when the reduce is folded into the RMSNorm that follows
 // (launch_gemm_residual_norm).  1 without partial planes.
+// True when `parts` partial planes of this GEMM (and as many rows of sums of squares) fit the
+// caller's workspace.
+static bool planes_fit(const GemmArgs& args, int parts) {
+    return args.split_partials != nullptr && parts * args.m * (static_cast<int64_t>(args.n) + 1) <= args.split_floats;
+}
+
 static int narrow_parts(const GemmArgs& args, bool fused_reduce) {
-    if (args.split_partials == nullptr) return 1;
+    if (!planes_fit(args, 2)) return 1;
     const int64_t blocks = static_cast<int64_t>(args.n / 64) * ((args.m + 63) / 64);
-    if (args.k % (32 * kSplitBlocksK) == 0 && blocks * kSplitBlocksK <= kNarrowSplitBlocks) return kSplitBlocksK;
+    if (args.k % (32 * kSplitBlocksK) == 0 && blocks * kSplitBlocksK <= kNarrowSplitBlocks &&
+        planes_fit(args, kSplitBlocksK))
+        return kSplitBlocksK;
     const int64_t cus = 256;
     const int64_t whole = (blocks + cus - 1) / cus;
     const int64_t halves = (2 * blocks + cus - 1) / cus;
@@ -1587,7 +1595,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         const dim3 split_block(64 * kSplitWaves);
         // Grids of at most a third of the device split K over kSplitBlocksK blocks when the
         // caller provides the partial planes.
-        const bool split_k = args.split_partials != nullptr &&
+        const bool split_k = planes_fit(args, kSplitBlocksK) &&
                              static_cast<int64_t>(grid.x) * grid.y * kSplitBlocksK <= kSplitKBlocks;
         if (split_k) grid.x *= kSplitBlocksK;
 #define FLUX_SPLIT_RT(E, ST, RT, NORM, COLS)                                                                        \

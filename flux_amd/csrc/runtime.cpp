@@ -613,6 +613,7 @@ PrefillRuntime::PrefillRuntime(const flux_weights& weights, const float* rope_co
     swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
     attn_workspace_ = reinterpret_cast<float*>(base + o_attn_ws);
     split_partials_ = split_k ? reinterpret_cast<float*>(base + o_split) : nullptr;
+    split_floats_ = split_k ? split_partials_floats(s, split_n) : 0;
     final_hidden_ = reinterpret_cast<float*>(base + o_final);
     logits_ = reinterpret_cast<float*>(base + o_logits);
     initial_token_ = reinterpret_cast<int64_t*>(base + o_token);
@@ -676,6 +677,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         float* values = db.value_cache + layer * layer_elems;
         GemmArgs qkv{};
         qkv.split_partials = split_partials_;
+        qkv.split_floats = split_floats_;
         qkv.b = weights_.packed_qkv[layer];
         qkv.m = seq_;
         qkv.n = kQKV;
@@ -700,6 +702,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
                   "launching prefill attention");
         GemmArgs o{};
         o.split_partials = split_partials_;
+        o.split_floats = split_floats_;
         o.a = attn_rows_;
         o.b = weights_.o_proj[layer];
         o.c = hidden_b_;
@@ -709,6 +712,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         o.k = kHidden;
         GemmArgs gu{};
         gu.split_partials = split_partials_;
+        gu.split_floats = split_floats_;
         gu.b = weights_.gate_up[layer];
         gu.c = swiglu_;
         gu.m = seq_;
@@ -727,6 +731,7 @@ void PrefillRuntime::run(const int64_t* input_ids, hipStream_t stream) {
         }
         GemmArgs dn{};
         dn.split_partials = split_partials_;
+        dn.split_floats = split_floats_;
         dn.a = swiglu_;
         dn.b = weights_.down[layer];
         dn.c = hidden_a_;

@@ -154,6 +154,7 @@ private:
     float* attn_rows_ = nullptr;  // [S, 576]
     float* attn_workspace_ = nullptr;  // split-key attention partials
     float* split_partials_ = nullptr;  // K-split GEMM partial planes (short prompts), or null
+    int64_t split_floats_ = 0;         // floats at split_partials_
     float* swiglu_ = nullptr;     // [S, 1536]
     float* final_hidden_ = nullptr;  // [576]
     float* logits_ = nullptr;     // [vocab]
