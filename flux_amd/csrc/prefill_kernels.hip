@@ -16,10 +16,13 @@
 //    interleaved 32+32 per group).  N = 576 outputs (o_proj, down) use 64x64 tiles.
 //    Grids smaller than the device (short prompts) use copy-ring variants, or, for
 //    K = 576 / 1536, a split-K kernel whose waves stream private LDS rings and which
-//    folds the preceding RMSNorm into the QKV and gate/up GEMMs.
+//    folds the preceding RMSNorm into the QKV and gate/up GEMMs.  Grids that leave CUs
+//    idle split K over blocks into partial planes, summed in order by a reduce kernel,
+//    or by the RMSNorm kernel that the next GEMM needs (split_reduce_residual_norm_kernel).
 //  * Attention: one block per (128-query tile, query head, key chunk); 4 waves x 32
 //    queries (prompts up to 512 tokens: one block per 32-query tile and head, its
-//    32-key chunks spread over 8 waves and combined in LDS).  S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x2f32, so the S^T
+//    32-key chunks spread over 8 waves and combined in LDS).  S^T = K Q^T and
+//    O^T += V^T P^T on v_mfma_f32_32x32x2f32, so the S^T
 //    accumulators are already the B operand of the PV product (no transpose).  The
 //    chunk length follows the prompt length; chunk partials are merged by a second
 //    kernel.
@@ -698,7 +701,7 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     }
 }
 
-// Sums the kSplitBlocksK partial planes of a K-split gemm_split_kernel in plane order and
+// Sums the kPlanes partial planes of a K-split gemm_split_kernel or gemm_narrow_kernel in plane order and
 // applies the epilogue: thread -> (row, column pair j / j + 32 of a 64-column group) for
 // kCols = 64, (row, column) for kCols = 32.  The folded norm's row scale comes from the
 // summed partial sums of squares.
