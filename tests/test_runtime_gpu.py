@@ -418,6 +418,44 @@ def test_decode_across_empty_position_chunks(small_model):
     assert runtime.device_error() == 0
 
 
+def test_decode_at_maximum_capacity_matches_prefill(small_model):
+    """The fused decode kernel at the largest capacity (16384 positions), where the position
+    chunks hold up to 193 rows and the attention takes its second 128-row pass (no other decode
+    test attends past 8704).  Teacher-forced steps from position 16380 to 16383 through replay():
+    the first and the last step's logits equal those of the native prefill of the prompt extended
+    by the fed tokens (the MFMA prefill path, independent of the decode GEMVs and of the decode
+    attention), and the K/V rows the decode wrote equal the prefill's rows in every layer."""
+    n_prompt, steps = 16380, 4
+    g = torch.Generator().manual_seed(16384)
+    tokens = torch.randint(0, 128, (1, n_prompt + steps), generator=g).cuda()
+    runtime = NativeSmolLM2Prefill.capture(small_model, tokens[:, :n_prompt], max_decode_steps=steps)
+    decoded = []
+    for step in range(steps):
+        logits = runtime.replay(tokens[:, n_prompt + step:n_prompt + step + 1])
+        decoded.append(logits[0, 0].float().cpu().clone())
+    torch.cuda.synchronize()
+    assert runtime.cache_position == n_prompt + steps
+    assert runtime.device_error() == 0
+    # Decode step s fed token n_prompt + s, so its logits are the prefill logits of n_prompt + s + 1 tokens.
+    for step in (0, steps - 1):
+        length = n_prompt + step + 1
+        reference = NativeSmolLM2Prefill.capture(small_model, tokens[:, :length], max_decode_steps=0)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(decoded[step], reference.logits[0, 0].float().cpu(), atol=LOGIT_ATOL,
+                                   rtol=LOGIT_RTOL, msg=lambda m: f"decode step {step} (attended {length}): {m}")
+        if step == steps - 1:
+            pos = length - 1
+            for layer in range(30):
+                torch.testing.assert_close(runtime.key_cache[layer, 0][:, pos].float().cpu(),
+                                           reference.key_cache[layer, 0][:, pos].float().cpu(),
+                                           rtol=KV_RTOL, atol=KV_ATOL)
+                torch.testing.assert_close(runtime.value_cache[layer, 0][:, pos].float().cpu(),
+                                           reference.value_cache[layer, 0][:, pos].float().cpu(),
+                                           rtol=KV_RTOL, atol=KV_ATOL)
+        del reference
+        torch.cuda.empty_cache()
+
+
 def test_wait_timeout_reports_error_and_invalid_tokens(small_model):
     """Failure handling, forced from the host: a zero bound on the fused kernel's
     cross-workgroup waits makes them give up at once (every kernel still exits normally).
