@@ -4,6 +4,11 @@ Each translation unit is compiled in parallel, then linked into one shared
 library whose C ABI is ``include/flux_amd.h``.  Usage::
 
     python -m flux_amd.build            # or flux_amd.build.build()
+    python -m flux_amd.build --trace    # also the timestamped decode library
+
+The ``--trace`` build defines ``FLUX_TRACE`` (decode phase timestamps, read by
+``flux_amd.trace_decode``) and writes ``flux_amd/lib/libflux_amd_trace.so``;
+the normal library is compiled without it and carries no trace code.
 """
 
 from __future__ import annotations
@@ -19,6 +24,7 @@ ROOT = os.path.dirname(PACKAGE)
 CSRC = os.path.join(PACKAGE, "csrc")
 LIB_DIR = os.path.join(PACKAGE, "lib")
 LIBRARY = os.path.join(LIB_DIR, "libflux_amd.so")
+TRACE_LIBRARY = os.path.join(LIB_DIR, "libflux_amd_trace.so")
 SOURCES = ("decode_kernels.hip", "prefill_kernels.hip", "eager_kernels.hip", "runtime.cpp", "capi.cpp")
 ARCH = os.environ.get("FLUX_AMD_ARCH", "gfx950")
 
@@ -40,9 +46,9 @@ def _flags() -> list[str]:
     ]
 
 
-def _compile(source: str, build_dir: str) -> str:
+def _compile(source: str, build_dir: str, defines: tuple[str, ...] = ()) -> str:
     obj = os.path.join(build_dir, os.path.splitext(source)[0] + ".o")
-    cmd = [hipcc(), *_flags()]
+    cmd = [hipcc(), *_flags(), *(f"-D{d}" for d in defines)]
     if source.endswith(".cpp"):
         cmd += ["-x", "hip"]
     cmd += ["-c", os.path.join(CSRC, source), "-o", obj]
@@ -56,22 +62,28 @@ def _compile(source: str, build_dir: str) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
-    """Compile every HIP translation unit and link the shared library."""
-    build_dir = os.path.join(ROOT, "_build")
+def build(verbose: bool = True, trace: bool = False) -> str:
+    """Compile every HIP translation unit and link the shared library.
+
+    ``trace=True`` builds the ``FLUX_TRACE`` variant into its own directory and
+    library file; it never replaces the normal library.
+    """
+    build_dir = os.path.join(ROOT, "_build", "trace") if trace else os.path.join(ROOT, "_build")
+    library = TRACE_LIBRARY if trace else LIBRARY
+    defines = ("FLUX_TRACE",) if trace else ()
     os.makedirs(build_dir, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as pool:
-        objects = list(pool.map(lambda s: _compile(s, build_dir), SOURCES))
-    tmp = LIBRARY + ".tmp"
+        objects = list(pool.map(lambda s: _compile(s, build_dir, defines), SOURCES))
+    tmp = library + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC", *objects, "-o", tmp]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"linking failed:\n{result.stdout}{result.stderr}")
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     if verbose:
-        print(f"built {LIBRARY}", flush=True)
-    return LIBRARY
+        print(f"built {library}", flush=True)
+    return library
 
 
 def build_oracle(verbose: bool = True) -> str | None:
@@ -90,4 +102,6 @@ def build_oracle(verbose: bool = True) -> str | None:
 if __name__ == "__main__":
     build()
     build_oracle()
+    if "--trace" in sys.argv[1:]:
+        build(trace=True)
     sys.exit(0)

@@ -402,6 +402,23 @@ __device__ __forceinline__ void qkv_unit_compute(const QkvUnitWeights& w, const 
 // Output per query head: o[64] (unnormalised), m, l.
 constexpr int kAttnScoreStride = 256;                // sp/pl row stride (positions)
 
+// Optional timestamps inside the attention and merge bodies and per wave around phase B's
+// K/V copy (compiled only with -DFLUX_TRACE; layer 15 of the third token of a launch).
+#ifdef FLUX_TRACE
+__device__ uint64_t g_flux_attn_trace[512][8];
+__device__ uint64_t g_flux_copy_trace[256][8][4];
+#define FLUX_ATTN_TRACE_PARAM , bool trace_on = false
+#define FLUX_ATTN_TRACE(k)                                                                            \
+    do {                                                                                              \
+        if (trace_on && tid_opaque() == 0) g_flux_attn_trace[blockIdx.x][k] = wall_clock64();        \
+    } while (0)
+#else
+#define FLUX_ATTN_TRACE_PARAM
+#define FLUX_ATTN_TRACE(k) \
+    do {                   \
+    } while (0)
+#endif
+
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ int attn_k_index(int r, int d) { return r * kHeadDim + 4 * ((d >> 2) ^ (r & 15)) + (d & 3); }
@@ -457,7 +474,8 @@ constexpr int kAttnRedFloats = kWavesPerWG * kGroup * kHeadDim + 4 * kGroup;
 // qv: the 3 query rows (LDS, 192 floats).  rows <= kAttnRows.  scale2 = scale*log2(e).
 template <class POut>
 __device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_lds, const float* qv, int rows,
-                                             float scale2, const AttnScratch& ws, const POut& out) {
+                                             float scale2, const AttnScratch& ws,
+                                             const POut& out FLUX_ATTN_TRACE_PARAM) {
     const int t = tid_opaque();
     const int lane = t & 63;
     const int wave = wave_uniform(t >> 6);
@@ -501,6 +519,7 @@ __device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_
         }
     }
     __syncthreads();
+    FLUX_ATTN_TRACE(0);
     // ---- scores, per-half maximum, probabilities ----
     float* red_ml = ws.red + kWavesPerWG * kGroup * kHeadDim;  // m[kGroup][2], l[kGroup][2]
     if (wave < 2 * kGroup) {
@@ -538,6 +557,7 @@ __device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_
         }
     }
     __syncthreads();
+    FLUX_ATTN_TRACE(1);
     // ---- PV: lane = dim over this wave's 16 positions ----
     {
         float o0 = 0.f, o1 = 0.f, o2 = 0.f;
@@ -577,6 +597,7 @@ __device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_
         dst[2 * kHeadDim] = o2;
     }
     __syncthreads();
+    FLUX_ATTN_TRACE(2);
     // ---- combine the 8 waves: halves rescaled to the chunk maximum ----
     if (wave < kGroup) {
         const int h = wave;
@@ -595,6 +616,7 @@ __device__ __forceinline__ void attn_compute(const float* k_lds, const float* v_
         }
     }
     __syncthreads();
+    FLUX_ATTN_TRACE(3);
 }
 
 // ---------------------------------------------------------------------------
@@ -806,10 +828,27 @@ __device__ uint64_t g_flux_trace_all[512][16];
             g_flux_trace[wg / 85][layer][slot] = wall_clock64();                                       \
         if (t == 2 && layer == 15 && tid_opaque() == 0) g_flux_trace_all[wg][slot] = wall_clock64();   \
     } while (0)
+#define FLUX_COPY_TRACE(k)                                                                            \
+    do {                                                                                              \
+        if (t == 2 && layer == 15 && (tid_opaque() & 63) == 0)                                        \
+            g_flux_copy_trace[wg][tid_opaque() >> 6][k] = wall_clock64();                              \
+    } while (0)
+#define FLUX_MERGE_TRACE(k)                                                                           \
+    do {                                                                                              \
+        if (t == 2 && layer == 15 && tid_opaque() == 0) g_flux_attn_trace[blockIdx.x][k] = wall_clock64(); \
+    } while (0)
+#define FLUX_TRACE_ARG , t == 2 && layer == 15
 #else
 #define FLUX_TRACE_POINT(slot) \
     do {                       \
     } while (0)
+#define FLUX_COPY_TRACE(k) \
+    do {                   \
+    } while (0)
+#define FLUX_MERGE_TRACE(k) \
+    do {                    \
+    } while (0)
+#define FLUX_TRACE_ARG
 #endif
 
 // ---------------------------------------------------------------------------
@@ -1015,8 +1054,10 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 float* v_lds = part + kAttnRows * kHeadDim;
                 // Waves 0-1 may still be finishing the QKV phase: waves 2-7 stage the cached
                 // rows and poll the query (and the current row) for the whole workgroup.
+                FLUX_COPY_TRACE(3);
                 attn_stage_lds(key_layer + g * head_stride, value_layer + g * head_stride, begin, cached_rows, k_lds,
                                v_lds, 2);
+                FLUX_COPY_TRACE(0);
                 const bool has_current = position >= begin && position < end;
                 const int cur = static_cast<int>(position - begin);
                 // Words 0..191: q of heads 3g..3g+2 -> vec; 192..255: new k row; 256..319: new v row.
@@ -1037,12 +1078,15 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                                                                 : v_lds + cur * kHeadDim + d;
                     },
                     2 * kWave, ep, wctx);
+                FLUX_COPY_TRACE(1);
                 __builtin_amdgcn_s_waitcnt(0);  // LDS-direct K/V loads have landed
+                FLUX_COPY_TRACE(2);
                 __syncthreads();
                 FLUX_TRACE_POINT(3);
                 attn_compute(k_lds, v_lds, vec, static_cast<int>(end - begin), Lw.scale * kLog2e,
                              AttnScratch{attn_sp, attn_pl, red},
-                             PartialLLOut{ll + LLLayout::kPartials + (g * tchunks + c) * partial_stride, ep});
+                             PartialLLOut{ll + LLLayout::kPartials + (g * tchunks + c) * partial_stride, ep}
+                                 FLUX_TRACE_ARG);
             }
 
             FLUX_TRACE_POINT(4);
@@ -1069,6 +1113,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 float M = -INFINITY;
                 for (int cc = lane; cc < tchunks; cc += kWave) M = fmaxf(M, part[cc * kRun + 16]);
                 M = wave_max_uniform(M);
+                FLUX_MERGE_TRACE(4);
                 // Wave w merges dims 2w (lanes 0-31) and 2w + 1 (lanes 32-63); lane slot
                 // s = lane % 32 sums chunks s, s + 32, ...
                 const int slot = lane & 31;
@@ -1090,6 +1135,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 L += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(L), kDppRowBcast15, 0xA, 0xF, false));
                 if ((lane & 31) == 31) red[d] = O / L;
                 __syncthreads();
+                FLUX_MERGE_TRACE(5);
                 // Thread (copy r = t / 16, dim d = t % 16) writes dim d of copy r: each copy's
                 // 16 dims are one 128-byte line written by one instruction.
                 if (tid_opaque() < 16 * LLLayout::kReplicas) {
@@ -1533,6 +1579,12 @@ size_t ll_arena_words() { return LLLayout::kTotal; }
 #ifdef FLUX_TRACE
 extern "C" int flux_debug_trace(uint64_t* host_out) {
     return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_trace), sizeof(g_flux_trace)));
+}
+extern "C" int flux_debug_attn_trace(uint64_t* host_out) {
+    return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_attn_trace), sizeof(g_flux_attn_trace)));
+}
+extern "C" int flux_debug_copy_trace(uint64_t* host_out) {
+    return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_copy_trace), sizeof(g_flux_copy_trace)));
 }
 extern "C" int flux_debug_trace_all(uint64_t* host_out) {
     return static_cast<int>(hipMemcpyFromSymbol(host_out, HIP_SYMBOL(g_flux_trace_all), sizeof(g_flux_trace_all)));
