@@ -420,15 +420,17 @@ def test_decode_across_empty_position_chunks(small_model):
     assert runtime.device_error() == 0
 
 
-def test_decode_at_maximum_capacity_matches_prefill(small_model):
-    """The fused decode kernel at the largest capacity (16384 positions), where the position
-    chunks hold up to 193 rows and the attention takes its second 128-row pass (no other decode
-    test attends past 8704).  Teacher-forced steps from position 16380 to 16383 through replay():
-    the first and the last step's logits equal those of the native prefill of the prompt extended
-    by the fed tokens (the MFMA prefill path, independent of the decode GEMVs and of the decode
-    attention), and the K/V rows the decode wrote equal the prefill's rows in every layer."""
-    n_prompt, steps = 16380, 4
-    g = torch.Generator().manual_seed(16384)
+@pytest.mark.parametrize("n_prompt,steps", [(5436, 8), (16380, 4)])
+def test_decode_matches_prefill_at_chunk_cap_and_capacity(small_model, n_prompt, steps):
+    """Teacher-forced decode steps through replay(): the first and the last step's logits equal
+    those of the native prefill of the prompt extended by the fed tokens (the MFMA prefill path,
+    independent of the decode GEMVs and of the decode attention), and the K/V rows the last step
+    wrote equal the prefill's rows in every layer.
+    - 5436 + 8: the attention splits the positions into one chunk per 64 up to its cap of 85
+      chunks, which it reaches at 5441 attended positions, inside this run (5437 to 5444).
+    - 16380 + 4: the largest capacity (16384 positions), where the chunks hold up to 193 rows
+      and the attention takes its second 128-row pass (no other decode test attends past 8704)."""
+    g = torch.Generator().manual_seed(n_prompt + steps)
     tokens = torch.randint(0, 128, (1, n_prompt + steps), generator=g).cuda()
     runtime = NativeSmolLM2Prefill.capture(small_model, tokens[:, :n_prompt], max_decode_steps=steps)
     decoded = []
