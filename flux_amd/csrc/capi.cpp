@@ -166,6 +166,8 @@ int flux_decode_device_error(flux_decode* runtime, int32_t* out) {
 
 int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks) {
     if (runtime == nullptr) return invalid("flux_decode_set_wait_limit: null argument");
+    if (ticks > FLUX_MAX_WAIT_TICKS)
+        return invalid("flux_decode_set_wait_limit: bound exceeds FLUX_MAX_WAIT_TICKS (1e9 ticks = 10 s)");
     runtime->impl->set_wait_limit(ticks);
     return FLUX_OK;
 }

@@ -42,6 +42,9 @@ extern "C" {
 #define FLUX_PACKED_QKV_WIDTH 960
 #define FLUX_PACKED_GATE_UP_WIDTH 3072
 #define FLUX_MAX_CAPACITY 16384
+/* Largest accepted bound of the fused decode kernel's cross-workgroup waits:
+ * 1e9 ticks of the 100 MHz wall clock = 10 s. */
+#define FLUX_MAX_WAIT_TICKS 1000000000ull
 
 enum flux_status {
     FLUX_OK = 0,
@@ -161,6 +164,9 @@ int flux_decode_device_error(flux_decode* runtime, int32_t* out);
  * flux_decode_generate_greedy launches (default 200 ms; the captured replay graph
  * keeps the default).  A wait that exceeds it records device error 1; the steps it
  * affects report token -1, and the next runtime call raises FLUX_ERROR_DEVICE.
+ * Bounds above FLUX_MAX_WAIT_TICKS (10 s) are rejected with
+ * FLUX_ERROR_INVALID_VALUE and leave the current bound unchanged, so every wait
+ * stays bounded.
  * No counterpart in the reference: the failure-handling test sets a tiny bound to
  * drive that path with every kernel still exiting normally. */
 int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks);

@@ -482,6 +482,12 @@ def test_wait_timeout_reports_error_and_invalid_tokens(small_model):
     assert runtime.device_error() == 1
     with pytest.raises(RuntimeError, match="device-side error 1"):
         runtime.replay(torch.tensor([[int(record["tokens"][0])]], device="cuda"))
+    # An unbounded wait is refused before it reaches the runtime (no launch), so every
+    # cross-workgroup wait stays bounded.
+    with pytest.raises(RuntimeError, match="FLUX_MAX_WAIT_TICKS"):
+        handle.set_wait_limit(2**64 - 1)
+    with pytest.raises(RuntimeError, match="FLUX_MAX_WAIT_TICKS"):
+        handle.set_wait_limit(1_000_000_001)
     handle.set_wait_limit(20_000_000)
     runtime.prefill(prompt)
     again = runtime.generate_greedy(n).clone()
