@@ -127,8 +127,7 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_decode_get_buffers", ctypes.c_int, [_vp, ctypes.POINTER(DecodeBuffers)]),
     ("flux_decode_device_error", ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int32)]),
     ("flux_decode_set_wait_limit", ctypes.c_int, [_vp, ctypes.c_uint64]),
-    ("flux_decode_cooperative_graph", ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int32)]),
-    ("flux_decode_graph_nodes", ctypes.c_int, [_vp, _i64, _i64]),
+    ("flux_decode_replay_launches", ctypes.c_int, [_vp, _i64, _i64]),
     ("flux_host_counters", ctypes.c_int, [_i64, _i64, _i64]),
     ("flux_decode_destroy", None, [_vp]),
     ("flux_prefill_create", ctypes.c_int,

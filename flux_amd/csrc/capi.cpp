@@ -172,11 +172,6 @@ int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks) {
     return FLUX_OK;
 }
 
-int flux_decode_cooperative_graph(const flux_decode* runtime, int32_t* out) {
-    if (runtime == nullptr || out == nullptr) return invalid("flux_decode_cooperative_graph: null argument");
-    *out = runtime->impl->cooperative_graph() ? 1 : 0;
-    return FLUX_OK;
-}
 
 void flux_decode_destroy(flux_decode* runtime) {
     if (runtime == nullptr || !runtime->owned) return;
@@ -438,10 +433,10 @@ int flux_embedding_gather_f32(const int64_t* ids, const float* embedding, int64_
                     "flux_embedding_gather_f32");
 }
 
-int flux_decode_graph_nodes(const flux_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes) {
-    if (runtime == nullptr || kernel_nodes == nullptr || total_nodes == nullptr)
-        return invalid("flux_decode_graph_nodes: null argument");
-    return guarded([&] { runtime->impl->graph_nodes(kernel_nodes, total_nodes); });
+int flux_decode_replay_launches(const flux_decode* runtime, int64_t* kernel_launches, int64_t* device_commands) {
+    if (runtime == nullptr || kernel_launches == nullptr || device_commands == nullptr)
+        return invalid("flux_decode_replay_launches: null argument");
+    return guarded([&] { runtime->impl->replay_launches(kernel_launches, device_commands); });
 }
 
 int flux_host_counters(int64_t* synchronizations, int64_t* allocations, int64_t* frees) {

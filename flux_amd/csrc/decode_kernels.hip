@@ -961,7 +961,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
         return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
     };
-    int64_t token = uniform64(*args.input_token);
+    int64_t token = uniform64(args.token_in != nullptr ? *args.token_in : *args.input_token);
     int64_t position = uniform64(*args.position);
     int64_t step = uniform64(*args.generation_step);
     __syncthreads();
@@ -1155,6 +1155,13 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 __syncthreads();  // the poll's wait also covered this wave's o_proj row copy
                 FLUX_TRACE_POINT(7);
                 if (active) {
+                    // This wave's o_proj row was copied into LDS by inline-asm LDS-direct loads
+                    // (phase B), which the compiler does not track.  The poll above already
+                    // waited for loads issued after them (every thread of waves 0-2 polls a
+                    // word while the vector is at least 3 waves wide); the explicit wait keeps
+                    // the dependency if the fetch changes, and costs nothing once it has.
+                    static_assert(kHidden >= 3 * kWave, "waves 0-2 must each poll a word of phase C's input");
+                    __builtin_amdgcn_s_waitcnt(0);
                     float w[9], a[9];
                     lds_slice576(oproj_rows[wave_uniform(static_cast<int>(tid_opaque() >> 6)) % 3], lane, w);
                     lds_slice576(vec, lane, a);

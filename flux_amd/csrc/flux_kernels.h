@@ -36,6 +36,9 @@ struct DecodeArgs {
     int64_t vocab;
     int64_t generated_capacity;
     int steps;
+    // When set, the launch's first step reads its input token here instead of from
+    // input_token (replay(token): the caller's token, read in stream order, no copy).
+    const int64_t* token_in;
 };
 
 // ---- fused decode ----

@@ -56,12 +56,13 @@ public:
     int64_t replay_count() const { return replay_count_; }
     int64_t capacity() const { return capacity_; }
     void buffers(flux_decode_buffers* out) const;
-    void graph_nodes(int64_t* kernels, int64_t* total) const;
+    // Kernel launches and all device commands (launches, event waits) issued by replay()
+    // since creation.
+    void replay_launches(int64_t* kernels, int64_t* commands) const;
     int device() const { return device_; }
     // Bound of every cross-workgroup wait of later generate_greedy launches, in 100 MHz
-    // wall-clock ticks (the captured replay graph keeps the bound it was captured with).
+    // wall-clock ticks (replays keep the default bound).
     void set_wait_limit(uint64_t ticks) { args_.wait_ticks = ticks; }
-    bool cooperative_graph() const { return cooperative_graph_; }
 
 private:
     void allocate();
@@ -72,6 +73,8 @@ private:
                           bool clear_outputs);
     void launch_steps(int64_t steps, hipStream_t stream, hipStream_t launch_stream);
     void release() noexcept;
+    // completion_, recorded on last_stream_ first when replays were queued after it.
+    hipEvent_t completion();
 
     int device_ = 0;
     int grid_ = 0;
@@ -102,7 +105,6 @@ private:
     int32_t* error_ = nullptr;
     int32_t* host_error_ = nullptr;         // mapped pinned host memory
     int32_t* host_error_device_ = nullptr;  // its device address
-    bool cooperative_graph_ = false;
     // Cooperative launches unless FLUX_DECODE_PLAIN_LAUNCH is set to a value other than 0
     // (profiling runs: rocprofv3 7.2 crashes at exit after cooperative launches).
     bool cooperative_ = true;
@@ -110,10 +112,11 @@ private:
     size_t state_bytes_ = 0;
     size_t ll_bytes_ = 0;
 
-    hipStream_t capture_stream_ = nullptr;
     hipEvent_t completion_ = nullptr;
-    hipGraph_t graph_ = nullptr;
-    hipGraphExec_t graph_exec_ = nullptr;
+    hipStream_t last_stream_ = nullptr;  // stream of the last queued work
+    bool completion_stale_ = false;      // work was queued on last_stream_ after completion_'s record
+    int64_t replay_kernels_ = 0;
+    int64_t replay_commands_ = 0;
     DecodeArgs args_{};
 };
 

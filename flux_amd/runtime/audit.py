@@ -3,11 +3,12 @@
 
 The reference profiles ten replays with ``torch.profiler`` and attributes CUDA
 events to owners by kernel-name heuristics.  Here each figure comes from the
-runtime itself: the launches per replay are the kernel nodes of the captured
-replay graph (``flux_decode_graph_nodes``), host synchronisations and device
-allocations are the runtime's own counters around the replays
-(``flux_host_counters``), and allocation growth is the device's free memory
-and torch's allocator before and after.  ``rocprofv3 --kernel-trace`` of
+runtime itself: the launches per replay are the growth of the runtime's own
+count of the kernel launches and device commands replay() issued
+(``flux_decode_replay_launches``) over the audited replays, host
+synchronisations and device allocations are the runtime's own counters around
+the replays (``flux_host_counters``), and allocation growth is the device's free
+memory and torch's allocator before and after.  ``rocprofv3 --kernel-trace`` of
 ``python -m flux_amd.runtime.audit`` confirms the launch count on the device.
 
 Usage: ``python -m flux_amd.runtime.audit [--capacity 4096] [--replays 10]``
@@ -43,7 +44,7 @@ class RuntimeAudit:
     stable_addresses: bool
     cpu_synchronize_events: int
     cpu_allocation_events: int
-    graph_nodes: int
+    device_commands_per_replay: float
     device_free_bytes_delta: int
     host_enqueue_us_per_replay: float
     device_us_per_replay: float
@@ -68,6 +69,8 @@ def runtime_audit(model: nn.Module, capacity: int = 4096, replays: int = 10) -> 
         native.replay()
     torch.cuda.synchronize()
     addresses = native.stable_addresses()
+    decode = native.native_object().decode
+    kernels_before, commands_before = decode.replay_launches()
     free_before = torch.cuda.mem_get_info(device)[0]
     allocated_before = torch.cuda.memory_allocated(device)
     syncs_before, allocs_before, frees_before = host_counters()
@@ -82,7 +85,8 @@ def runtime_audit(model: nn.Module, capacity: int = 4096, replays: int = 10) -> 
     syncs_after, allocs_after, frees_after = host_counters()
     allocated_after = torch.cuda.memory_allocated(device)
     free_after = torch.cuda.mem_get_info(device)[0]
-    kernels, nodes = native.native_object().decode.graph_nodes()
+    kernels_after, commands_after = decode.replay_launches()
+    kernels = (kernels_after - kernels_before) // replays
     result = RuntimeAudit(
         capacity=capacity,
         replays=replays,
@@ -94,7 +98,7 @@ def runtime_audit(model: nn.Module, capacity: int = 4096, replays: int = 10) -> 
         stable_addresses=addresses == native.stable_addresses(),
         cpu_synchronize_events=syncs_after - syncs_before,
         cpu_allocation_events=(allocs_after - allocs_before) + (frees_after - frees_before),
-        graph_nodes=nodes,
+        device_commands_per_replay=(commands_after - commands_before) / replays,
         device_free_bytes_delta=free_after - free_before,
         host_enqueue_us_per_replay=round(enqueue * 1e6 / replays, 2),
         device_us_per_replay=round(start.elapsed_time(stop) * 1e3 / replays, 2),

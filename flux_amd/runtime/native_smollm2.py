@@ -222,10 +222,11 @@ class _DecodeHandle:
         _native.check(_native.load().flux_decode_replay_count(self.raw, ctypes.byref(out)))
         return int(out.value)
 
-    def graph_nodes(self) -> tuple[int, int]:
-        """(kernel nodes, all nodes) of the captured one-step replay graph."""
+    def replay_launches(self) -> tuple[int, int]:
+        """(kernel launches, all device commands) issued by replay() since creation."""
         kernels, total = ctypes.c_int64(), ctypes.c_int64()
-        _native.check(_native.load().flux_decode_graph_nodes(self.raw, ctypes.byref(kernels), ctypes.byref(total)))
+        _native.check(_native.load().flux_decode_replay_launches(self.raw, ctypes.byref(kernels),
+                                                                 ctypes.byref(total)))
         return int(kernels.value), int(total.value)
 
     def replay(self, token: torch.Tensor | None) -> torch.Tensor:
@@ -234,9 +235,16 @@ class _DecodeHandle:
                     or not token.is_contiguous():
                 raise RuntimeError("flux native full decode: replay token has shape "
                                    f"{tuple(token.shape)}, expected [1, 1] contiguous long on {self.device}")
-        with torch.cuda.device(self.device):
-            _native.check(_native.load().flux_decode_replay(
-                self.raw, _native.ptr(token), _native.current_stream(self.device), None))
+        address = None if token is None else token.data_ptr()
+        lib = _native.load()
+        if torch.cuda.current_device() == self.device.index:
+            # Per-token path: the runtime's device is current, so no device switch is needed.
+            status = lib.flux_decode_replay(self.raw, address, torch.cuda.current_stream().cuda_stream, None)
+        else:
+            with torch.cuda.device(self.device):
+                status = lib.flux_decode_replay(self.raw, address, _native.current_stream(self.device), None)
+        if status != _native.FLUX_OK:
+            _native.check(status)
         return self.logits
 
     def generate_greedy(self, steps: int) -> torch.Tensor:
@@ -262,11 +270,6 @@ class _DecodeHandle:
         """Bound (100 MHz ticks) of the cross-workgroup waits of later generate_greedy launches."""
         _native.check(_native.load().flux_decode_set_wait_limit(self.raw, int(ticks)))
 
-    def cooperative_graph(self) -> bool:
-        """Whether the captured replay graph's kernel node is a cooperative launch."""
-        out = ctypes.c_int32()
-        _native.check(_native.load().flux_decode_cooperative_graph(self.raw, ctypes.byref(out)))
-        return bool(out.value)
 
 
 class _PrefillHandle:
@@ -598,7 +601,7 @@ class NativeSmolLM2Decode:
             raise ValueError("each layer's K and V source shapes must match")
 
     def replay(self, token: torch.Tensor | None = None) -> torch.Tensor:
-        """Asynchronously enqueue an optional token copy and one graph launch."""
+        """Asynchronously enqueue one launch of the fused step kernel (it reads ``token`` itself)."""
         return self._handle.replay(token)
 
     def generate_greedy(self, decode_steps: int) -> torch.Tensor:

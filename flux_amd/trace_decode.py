@@ -94,6 +94,14 @@ def trace_launch(lib: ctypes.CDLL) -> list[str]:
     durations = np.diff(layer_starts[:31]) / TICKS_PER_US
     lines.append("")
     lines.append("workgroup 0, layer durations (us, layers 0-29): " + " ".join(f"{d:.2f}" for d in durations))
+    # The final phase (slot row 30): start, final-norm input fetched with the first LM-head
+    # rows requested, the workgroup's argmax done, the token chosen from every workgroup's.
+    lm = per_layer[:, 30, :4]
+    start = int(lm[:, 0][lm[:, 0] > 0].min())
+    for name, slot in (("final h fetched", 1), ("workgroup argmax", 2), ("token chosen", 3)):
+        us = (lm[:, slot][lm[:, slot] > 0] - start) / TICKS_PER_US
+        lines.append(f"LM head phase, {name}: " + " ".join(f"{u:.2f}" for u in us) +
+                     " us after its start (workgroups 0, 85, 170, 255)")
     return lines
 
 

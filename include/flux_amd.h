@@ -121,21 +121,28 @@ const char* flux_version(void);
  *  native_decode_runtime_torch.cpp:38-79).
  * key_sources/value_sources: per layer [1, 3, source_lengths[i], 64] contiguous
  * float32 with source_lengths[i] >= position; may be NULL when position == 0.
- * Builds the stable buffers, imports the cache, and captures one decode step in
- * a hipGraph.  `stream` orders the setup (the reference's current stream). */
+ * Builds the stable buffers, imports the cache and runs one warm-up step (the
+ * reference warms its step before capturing it).  `stream` orders the setup (the
+ * reference's current stream). */
 int flux_decode_create(const flux_weights* weights, const float* rope_cos, const float* rope_sin, int64_t capacity,
                        int64_t position, const int64_t* initial_token, const float* const* key_sources,
                        const float* const* value_sources, const int64_t* source_lengths, const double* epsilons,
                        const double* attention_scales, hipStream_t stream, flux_decode** out);
 
-/* One decode step: optional token copy (device [1,1] int64, may be NULL), then
- * graph replay; returns the logits buffer.  (native_decode_runtime_cuda.cu:907-931)
+/* One decode step; returns the logits buffer.  (native_decode_runtime_cuda.cu:907-931,
+ * which copies the token and replays a CUDA graph of ~300 launches.)  Here the whole
+ * step is one kernel, launched directly: `token` (device [1,1] int64, or NULL for the
+ * fed-back argmax) is read by the step itself in stream order, so there is no copy.
  * Like flux_decode_generate_greedy, it first returns FLUX_ERROR_DEVICE when an
  * earlier launch that has finished reported a device-side error (non-blocking
  * check of a host-visible error word); prefill or reset re-arms the runtime.
- * The fused kernel needs every workgroup resident at once (one per CU): direct
- * launches are cooperative and fail when that cannot hold; the GPU must not be
- * shared with other work while a launch runs. */
+ * The fused kernel needs every workgroup resident at once (one per CU):
+ * flux_decode_generate_greedy launches cooperatively (a grid that cannot be
+ * co-resident fails at launch); a replay launches plainly (a cooperative launch
+ * costs ~20 us per token), and a step that starts while other work holds CUs
+ * reports device error 1 through its bounded waits instead of hanging.  `stream`
+ * must stay valid until the runtime's next call on another stream, synchronising
+ * call or destruction (the completion event is recorded then). */
 int flux_decode_replay(flux_decode* runtime, const int64_t* token, hipStream_t stream, float** logits);
 
 /* `decode_steps` greedy steps in one launch of the fused decode kernel; returns
@@ -161,8 +168,7 @@ int flux_decode_get_buffers(const flux_decode* runtime, flux_decode_buffers* out
 int flux_decode_device_error(flux_decode* runtime, int32_t* out);
 
 /* Bound, in 100 MHz wall-clock ticks, of every cross-workgroup wait of later
- * flux_decode_generate_greedy launches (default 200 ms; the captured replay graph
- * keeps the default).  A wait that exceeds it records device error 1; the steps it
+ * flux_decode_generate_greedy launches (default 200 ms; replays keep the default).  A wait that exceeds it records device error 1; the steps it
  * affects report token -1, and the next runtime call raises FLUX_ERROR_DEVICE.
  * Bounds above FLUX_MAX_WAIT_TICKS (10 s) are rejected with
  * FLUX_ERROR_INVALID_VALUE and leave the current bound unchanged, so every wait
@@ -171,15 +177,12 @@ int flux_decode_device_error(flux_decode* runtime, int32_t* out);
  * drive that path with every kernel still exiting normally. */
 int flux_decode_set_wait_limit(flux_decode* runtime, uint64_t ticks);
 
-/* *out = 1 when the captured replay graph's kernel node is a cooperative launch
- * (its workgroups are guaranteed co-resident or the launch fails), else 0.
- * No counterpart in the reference (its decode step is ordinary launches). */
-int flux_decode_cooperative_graph(const flux_decode* runtime, int32_t* out);
 /* Time the next `decode_steps` steps with events on `stream` (benchmark aid). */
-/* Nodes of the captured replay graph: kernel nodes (the launches per replay) and all
- * nodes.  Counterpart of the launch count the reference's runtime audit takes with
+/* Kernel launches and all device commands (launches, cross-stream event waits)
+ * issued by flux_decode_replay since creation; the audit divides their growth by the
+ * replays.  Counterpart of the launch count the reference's runtime audit takes with
  * torch.profiler (benchmarks/benchmark_flux.py:818-859). */
-int flux_decode_graph_nodes(const flux_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes);
+int flux_decode_replay_launches(const flux_decode* runtime, int64_t* kernel_launches, int64_t* device_commands);
 /* Process-wide totals since load of the runtimes' host-blocking calls (stream/event
  * synchronisation, synchronous copies), device allocations and frees; the audit
  * compares them around replays (benchmarks/benchmark_flux.py:838-858). */

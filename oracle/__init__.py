@@ -24,6 +24,8 @@ Pinning (what checks each function; see ``tests/test_oracle.py``):
   mean-of-V closed form, single-position -> V row.
 * ``kernels.greedy_argmax`` -- ties to lowest index, NaN-is-max, all -inf -> 0
   (cases of ``csrc/tests/test_greedy_generation.cu:46-103``).
-* ``kernels.causal_attention`` -- zero query -> prefix mean of V, agreement
-  with ``torch.softmax`` on a materialised score matrix.
+* ``kernels.causal_attention`` -- zero query -> prefix mean of V; row 0 -> the
+  V row of key 0; every checked row t equals ``gqa_decode_attention`` over the
+  prefix [0, t] (itself checked against ``torch.softmax`` with repeat_kv), which
+  fixes the scale, the mask and the head grouping; a planted scale mistake fails.
 """

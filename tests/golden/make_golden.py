@@ -24,6 +24,11 @@ synthetic weights, and stores small vectors under ``tests/golden/``:
                         changes at every step is fed one token at a time; per-step
                         probes, full logits at the first and last steps and around
                         the middle, and every layer's K/V rows at the fed positions.
+* ``tail_ctx8192.npz``  config 5's last 32 positions with changing tokens: after the
+                        8192-token prompt, 480 greedy steps, then 32 seeded teacher tokens
+                        at positions 8672..8703; top-8 logits at every step, probes in the
+                        window, full logits at its first and last steps and every layer's K/V
+                        rows at its first, middle and last fed positions.
 * ``permuted.npz``      free-running greedy stream of the untied permuted-head model
                         (``synthetic.PERMUTED_HEAD_SPEC``), whose token changes at
                         every step: 64 tokens with per-step probes and full logits
@@ -72,16 +77,17 @@ def step_probes(logits: torch.Tensor, top: int = 64) -> dict[str, np.ndarray]:
 
 
 def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int, *, probe_steps=None, teacher=None,
-                       full_logit_steps=(), kv_steps=()):
+                       full_logit_steps=(), kv_steps=(), free_steps=0):
     """Greedy (or teacher-forced) decode with HF, recording per-step probes and K/V slices.
 
-    Step 0's logits come from the prompt; step s >= 1 feeds ``teacher[s-1]`` when a
-    teacher sequence is given, else the previous step's argmax.  ``probe_steps``
+    Step 0's logits come from the prompt; step s >= 1 feeds ``teacher[s-1-free_steps]``
+    when a teacher sequence is given and s > free_steps, else the previous step's argmax
+    (so ``free_steps`` greedy steps run before the teacher window).  ``probe_steps``
     (default: every step) get the top-64 and 256-index probe; every step gets the
     token, the margin and the top-8.  ``full_logit_steps`` keep the whole logit
     row; ``kv_steps`` keep every layer's K/V row written by that step's token.
     """
-    steps = new_tokens if teacher is None else len(teacher) + 1
+    steps = new_tokens if teacher is None else free_steps + len(teacher) + 1
     probe_steps = list(range(steps)) if probe_steps is None else [s for s in probe_steps if s < steps]
     with torch.inference_mode():
         out = model(input_ids=prompt, use_cache=True, logits_to_keep=1)
@@ -110,7 +116,7 @@ def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int, *, probe_st
             tokens.append(token)
             if step + 1 == steps:
                 break
-            fed = token if teacher is None else int(teacher[step])
+            fed = token if teacher is None or step < free_steps else int(teacher[step - free_steps])
             out = model(input_ids=torch.tensor([[fed]]), past_key_values=cache, use_cache=True,
                         logits_to_keep=1)
             cache = out.past_key_values
@@ -133,6 +139,7 @@ def greedy_with_probes(model, prompt: torch.Tensor, new_tokens: int, *, probe_st
         record[key] = np.stack([p[key] for p in probes])
     if teacher is not None:
         record["teacher"] = np.asarray(teacher, dtype=np.int64)
+        record["free_steps"] = np.int64(free_steps)
     if full_logit_steps:
         record["full_logit_steps"] = np.asarray([s for s in full_logit_steps if s < steps], dtype=np.int64)
         record["full_logits"] = np.stack(full)
@@ -244,7 +251,7 @@ def main(selected: set[str]) -> None:
 
     for length in CONTEXT_LENGTHS:
         name = f"ctx{length}"
-        if not want(name) and not (length == 8192 and want("teacher_ctx8192")):
+        if not want(name) and not (length == 8192 and (want("teacher_ctx8192") or want("tail_ctx8192"))):
             continue
         prompt = synthetic.synthetic_prompt(2, length)
         if want(name):
@@ -255,6 +262,18 @@ def main(selected: set[str]) -> None:
             np.savez_compressed(os.path.join(OUT, f"{name}.npz"), **record)
             print(f"{name} done in {time.time() - t:.1f}s tokens={sorted(set(record['tokens'].tolist()))} "
                   f"min margin={record['margin'].min():.4f}", flush=True)
+        if length == 8192 and want("tail_ctx8192"):
+            # Config 5's last 32 positions (8672..8703) with changing tokens: 480 greedy steps
+            # after the 8192-token prompt, then 32 teacher-forced ones.
+            t = time.time()
+            teacher = teacher_tokens(3, 32)
+            free = CONFIG5_STEPS - 1 - len(teacher)
+            record = greedy_with_probes(model, prompt, 0, teacher=teacher, free_steps=free,
+                                        probe_steps=(free, free + 1, free + 16, free + 32),
+                                        full_logit_steps=(free + 1, free + 32),
+                                        kv_steps=(free + 1, free + 16, free + 32))
+            np.savez_compressed(os.path.join(OUT, "tail_ctx8192.npz"), **record)
+            print(f"tail_ctx8192 done in {time.time() - t:.1f}s", flush=True)
         if length == 8192 and want("teacher_ctx8192"):
             t = time.time()
             teacher = teacher_tokens(2, 32)

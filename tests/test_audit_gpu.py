@@ -17,7 +17,9 @@ pytestmark = pytest.mark.gpu
 def test_decode_replay_audit(small_model):
     audit = runtime_audit(small_model, capacity=4096, replays=10)
     assert audit.launches_per_replay == 1 and audit.flux_launches_per_replay == 1
-    assert audit.graph_nodes == 1
+    # The replay is that one launch: no token copy, and no event wait between replays on
+    # one stream.
+    assert audit.device_commands_per_replay == 1
     assert audit.cublas_launches_per_replay == 0 and audit.framework_launches_per_replay == 0
     assert audit.replay_allocation_growth_bytes == 0 and audit.device_free_bytes_delta == 0
     assert audit.stable_addresses

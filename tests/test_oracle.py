@@ -307,6 +307,14 @@ def test_causal_attention_closed_forms():
     out = ref.causal_attention(q, k, v, 0.125)
     for h in range(9):  # row 0 attends only to key 0
         torch.testing.assert_close(out[h, 0], v[h // 3, 0].double())
+    # Every row t equals the one-token GQA over the prefix [0, t] (gqa_decode_attention is
+    # pinned to torch.softmax with repeat_kv above): this fixes the scale, the causal
+    # mask and the head grouping of every row, the last row included.
+    for t in (1, 7, 19):
+        torch.testing.assert_close(out[:, t], ref.gqa_decode_attention(q[:, t], k, v, t + 1, 0.125))
+    # A planted scale mistake (scores scaled by 1/4 instead of 1/8) misses that check.
+    wrong = ref.causal_attention(q, k, v, 0.25)
+    assert not torch.allclose(wrong[:, 19], ref.gqa_decode_attention(q[:, 19], k, v, 20, 0.125))
 
 
 def test_gate_up_swiglu_closed_form():

@@ -204,6 +204,37 @@ def test_teacher_forced_changing_tokens(smol_model, name):
     assert runtime.device_error() == 0
 
 
+def test_replays_queued_without_synchronising_keep_their_tokens(smol_model):
+    """replay(token) passes the caller's token pointer to the step itself (no copy): the 48
+    teacher tokens, each in its own tensor, are queued back to back with no synchronisation,
+    so the step arguments change while earlier steps are still queued.  Every layer's K/V row
+    at the fed positions and the last step's logits must still equal the teacher-forced golden
+    (a step that read a later step's token would write a different K/V row)."""
+    record = golden("teacher_config1.npz")
+    teacher = record["teacher"].tolist()
+    runtime = _capture(smol_model, record, len(teacher))
+    prompt_len = len(record["prompt"])
+    tokens = [torch.tensor([[t]], dtype=torch.long, device="cuda") for t in teacher]
+    for token in tokens:
+        runtime.replay(token)
+    torch.cuda.synchronize()
+    _check_step(runtime.native_object().decode.logits[0, 0], record, len(teacher))
+    for i, step in enumerate(record["kv_steps"].tolist()):
+        pos = prompt_len + step - 1
+        torch.testing.assert_close(runtime.key_cache[:, 0, :, pos].float().cpu(),
+                                   torch.from_numpy(record["kv_step_k"][i]), rtol=KV_RTOL, atol=KV_ATOL)
+        torch.testing.assert_close(runtime.value_cache[:, 0, :, pos].float().cpu(),
+                                   torch.from_numpy(record["kv_step_v"][i]), rtol=KV_RTOL, atol=KV_ATOL)
+    # Mixing replay(None) (the fed-back argmax) with the same token tensor reused.
+    runtime.prefill(torch.from_numpy(record["prompt"]).unsqueeze(0).cuda())
+    runtime.replay(tokens[0])
+    runtime.replay(tokens[1])
+    runtime.replay(tokens[1])
+    torch.cuda.synchronize()
+    assert runtime.cache_position == prompt_len + 3
+    assert runtime.device_error() == 0
+
+
 def test_permuted_head_free_running_stream(permuted_model):
     """Untied permuted-head model: the HF greedy stream changes at every step, so each decode
     step's input is the previous step's on-device argmax.  64 tokens from one generate_greedy
@@ -263,6 +294,51 @@ def test_config5_8192_plus_512_steps(smol_model):
     torch.cuda.synchronize()
     assert torch.equal(first, second)
     assert torch.equal(logits_first, _decode_logits(runtime))
+    assert runtime.device_error() == 0
+
+
+def test_config5_every_step_logits(smol_model):
+    """Config 5 replayed step by step: after the 8192-token prefill, replay(token) feeds HF's
+    greedy stream for 512 steps (positions 8192..8703); every step's top-8 logits match HF's,
+    and the probe steps their top-64 and 256-index probe."""
+    record = golden("ctx8192.npz")
+    runtime = _capture(smol_model, record, 512)
+    _replay_stream(runtime, record, record["tokens"].tolist(), 513)
+    assert runtime.cache_length == 8704
+    assert runtime.device_error() == 0
+
+
+def test_config5_tail_with_changing_tokens(smol_model):
+    """Config 5's last 32 positions with changing tokens: after the 8192-token prefill, one
+    generate_greedy(481) call runs 480 decode steps free (positions 8192..8671, tokens equal
+    HF's), then replay(token) feeds 32 seeded tokens that change at every step at positions
+    8672..8703 (the cache ends at 8704).  Every step's top-8 logits, the window's probes, all
+    49152 logits at its first and last steps and every layer's K/V rows at its first, middle
+    and last fed positions match HF."""
+    record = golden("tail_ctx8192.npz")
+    free = int(record["free_steps"])
+    teacher = record["teacher"].tolist()
+    assert all(a != b for a, b in zip(teacher, teacher[1:]))
+    runtime = _capture(smol_model, record, free + len(teacher))
+    prompt_len = len(record["prompt"])
+    generated = runtime.generate_greedy(free + 1).clone()
+    torch.cuda.synchronize()
+    assert generated[0].cpu().numpy().tolist() == record["tokens"][:free + 1].tolist()
+    _check_step(_decode_logits(runtime), record, free)
+    kv_steps = record["kv_steps"].tolist()
+    for i, token in enumerate(teacher):
+        step = free + 1 + i
+        logits = runtime.replay(torch.tensor([[token]], dtype=torch.long, device="cuda"))
+        torch.cuda.synchronize()
+        _check_step(logits[0, 0], record, step)
+        if step in kv_steps:
+            j = kv_steps.index(step)
+            pos = prompt_len + step - 1
+            torch.testing.assert_close(runtime.key_cache[:, 0, :, pos].float().cpu(),
+                                       torch.from_numpy(record["kv_step_k"][j]), rtol=KV_RTOL, atol=KV_ATOL)
+            torch.testing.assert_close(runtime.value_cache[:, 0, :, pos].float().cpu(),
+                                       torch.from_numpy(record["kv_step_v"][j]), rtol=KV_RTOL, atol=KV_ATOL)
+    assert runtime.cache_length == prompt_len + free + len(teacher) == 8704
     assert runtime.device_error() == 0
 
 
@@ -470,7 +546,6 @@ def test_wait_timeout_reports_error_and_invalid_tokens(small_model):
     n = len(record["tokens"])
     runtime = NativeSmolLM2Prefill.capture(small_model, prompt, max_decode_steps=n - 1)
     handle = runtime.native_object().decode
-    assert isinstance(handle.cooperative_graph(), bool)
     first = runtime.generate_greedy(n).clone()
     torch.cuda.synchronize()
     assert first[0].cpu().numpy().tolist() == record["tokens"].tolist()

@@ -25,6 +25,11 @@ class _FakeTraceLibrary:
         copies[:255, :, :] = 1500
         per_layer = np.zeros((4, 31, 16), dtype=np.uint64)
         per_layer[0, :, 0] = 1000 + 1450 * np.arange(31)  # 14.5 us layers
+        # Final phase (row 30) of the four traced workgroups: start, h fetched, argmax, token.
+        per_layer[:, 30, 0] = 1000 + 1450 * 30
+        per_layer[:, 30, 1] = 1000 + 1450 * 30 + 160 + np.arange(4)
+        per_layer[:, 30, 2] = 1000 + 1450 * 30 + 1800
+        per_layer[:, 30, 3] = 1000 + 1450 * 30 + 2100
         self.buffers = {
             "flux_debug_trace_all": phases,
             "flux_debug_attn_trace": attention,
@@ -58,7 +63,10 @@ def test_trace_table_times_are_relative_to_the_first_phase_a_start():
     assert _row(lines, "attention QK^T done") == ["attention QK^T done", "10.00", "10.00", "10.00", "255"]
     assert _row(lines, "merge global max done")[1:] == ["20.00", "20.00", "20.00", "36"]
     assert _row(lines, "K/V copy landed, wave 7")[1:] == ["5.00", "5.00", "5.00", "255"]
-    assert lines[-1].endswith(" ".join(["14.50"] * 30))
+    [durations] = [line for line in lines if line.startswith("workgroup 0, layer durations")]
+    assert durations.endswith(" ".join(["14.50"] * 30))
+    assert lines[-3].startswith("LM head phase, final h fetched: 1.60 1.61 1.62 1.63 us")
+    assert lines[-1].startswith("LM head phase, token chosen: 21.00 21.00 21.00 21.00 us")
 
 
 def test_trace_buffers_match_the_kernel_declarations():
