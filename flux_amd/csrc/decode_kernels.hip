@@ -211,17 +211,6 @@ struct LLIn {
     }
 };
 
-struct PlainOut {
-    float* p;
-    __device__ __forceinline__ void put(int i, float v) const { p[i] = v; }
-};
-
-struct LLOut {
-    uint64_t* p;
-    uint32_t epoch;
-    __device__ __forceinline__ void put(int i, float v) const { ll_store(p + i, v, epoch); }
-};
-
 // QKV outputs: `v` is the same in every lane; the LL form writes every copy of the
 // replicated q/k/v vector (p = copy 0), the plain form writes once from lane 0.
 struct QkvPlainOut {
@@ -244,13 +233,6 @@ __device__ __forceinline__ void fetch_slice576(const In& in, int lane, float (&v
     in.fetch(idx, v);
 }
 
-template <class In>
-__device__ __forceinline__ float fetch_one(const In& in, int i) {
-    int idx[1] = {i};
-    float v[1];
-    in.fetch(idx, v);
-    return v[0];
-}
 
 // Normalised 576-slice with the norm weights already in registers.
 __device__ __forceinline__ void norm_slice_w(const float (&h)[9], const float (&wn)[9], float eps, float (&x)[9]) {
@@ -631,53 +613,6 @@ struct PartialLLOut {
     __device__ __forceinline__ void put(int h, int j, float v) const { ll_store(p + h * (kHeadDim + 2) + j, v, epoch); }
 };
 
-// Phase B2: merge `chunks` partials of one query head.  Wave w handles partials
-// c = w, w+8, ...; lane = dim.  Returns (in lane-dim of thread < 64) the
-// normalised output via `out.put(dim, value)`.
-template <class In, class Out>
-__device__ __forceinline__ void merge_head(const In& in, int chunks, int64_t partial_stride, float* red,
-                                           const Out& out) {
-    const int lane = tid_opaque() & 63;
-    const int wave = tid_opaque() >> 6;
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int c = wave; c < chunks; c += kWavesPerWG) {
-        const int base = static_cast<int>(c * partial_stride);
-        const int idx[3] = {base + lane, base + kHeadDim, base + kHeadDim + 1};
-        float v[3];
-        in.fetch(idx, v);
-        const float mc = v[1];
-        if (mc == -INFINITY) continue;
-        const float nm = fmaxf(M, mc);
-        const float a = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
-        const float b = fast_exp2(mc - nm);
-        O = O * a + v[0] * b;
-        L = L * a + v[2] * b;
-        M = nm;
-    }
-    float* red_m = red;
-    float* red_l = red + kWavesPerWG;
-    float* red_o = red + 2 * kWavesPerWG;
-    red_o[wave * kHeadDim + lane] = O;
-    if (lane == 0) {
-        red_m[wave] = M;
-        red_l[wave] = L;
-    }
-    __syncthreads();
-    if (tid_opaque() < kHeadDim) {
-        float mm = -INFINITY;
-        for (int w = 0; w < kWavesPerWG; ++w) mm = fmaxf(mm, red_m[w]);
-        float acc = 0.0f, lsum = 0.0f;
-        for (int w = 0; w < kWavesPerWG; ++w) {
-            if (red_m[w] == -INFINITY) continue;
-            const float f = fast_exp2(red_m[w] - mm);
-            acc += red_o[w * kHeadDim + tid_opaque()] * f;
-            lsum += red_l[w] * f;
-        }
-        out.put(tid_opaque(), acc / lsum);
-    }
-    __syncthreads();
-}
-
 // Chunking of the attended positions [0, L) across `chunks` workgroups.
 __device__ __forceinline__ void chunk_range(int64_t attended, int chunks, int c, int64_t& begin, int64_t& end) {
     const int64_t per = (attended + chunks - 1) / chunks;
@@ -748,16 +683,6 @@ __device__ __forceinline__ void lm_rows_pipelined(const float* __restrict__ lm_h
         const bool next_a = base + 2 * kLmBatch < row1;
         if (next_a) lm_load(lm_head, base + 2 * kLmBatch, row1, lane, wa);
         lm_stage(x, wb, base + kLmBatch, row1, logits, best_v, best_i);
-    }
-}
-
-template <class LogitsOut>
-__device__ __forceinline__ void lm_rows(const float* __restrict__ lm_head, const float (&x)[9], int64_t row0, int64_t row1,
-                                        int lane, const LogitsOut& logits, float& best_v, int64_t& best_i) {
-    for (int64_t base = row0; base < row1; base += kLmBatch) {
-        float w[kLmBatch][9];
-        lm_load(lm_head, base, row1, lane, w);
-        lm_stage(x, w, base, row1, logits, best_v, best_i);
     }
 }
 
@@ -1388,14 +1313,49 @@ __global__ void __launch_bounds__(kThreads) attn_partial_kernel(const float* q_p
                  PartialPlainOut{partials + (g * chunks + c) * kGroup * (kHeadDim + 2)});
 }
 
+// Merge of one query head's chunk partials.  Every partial word of the head is requested
+// at once into LDS (one memory round trip; a loop that loads chunk after chunk waits for
+// one round trip per iteration), then thread (dim d = t % 64, slot s = t / 64) sums the
+// chunks s, s + 8, ... with weights 2^(m_c - M), and the 8 slots are added in order.
 __global__ void __launch_bounds__(kThreads) attn_merge_kernel(const float* partials, int chunks, float* out) {
-    __shared__ float red[2 * kWavesPerWG + kWavesPerWG * kHeadDim];
+    __shared__ float red_o[kWavesPerWG][kHeadDim];
+    __shared__ float red_l[kWavesPerWG];
+    extern __shared__ float staged[];  // chunks * 66: o[64], m, l per chunk
     const int h = blockIdx.x;
     const int g = h / kGroup;
     const int hh = h % kGroup;
-    const int64_t stride = kGroup * (kHeadDim + 2);
-    merge_head(PlainIn{partials + g * chunks * stride + hh * (kHeadDim + 2)}, chunks, stride, red,
-               PlainOut{out + h * kHeadDim});
+    const int lane = tid_opaque() & 63;
+    const int wave = tid_opaque() >> 6;
+    constexpr int kRow = kHeadDim + 2;
+    const float* src = partials + static_cast<int64_t>(g) * chunks * kGroup * kRow + hh * kRow;
+    for (int k = tid_opaque(); k < chunks * kRow; k += kThreads) {
+        const int c = k / kRow;
+        staged[k] = src[static_cast<int64_t>(c) * kGroup * kRow + (k - c * kRow)];
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    for (int c = lane; c < chunks; c += kWave) M = fmaxf(M, staged[c * kRow + kHeadDim]);
+    M = wave_max_uniform(M);
+    float O = 0.0f, L = 0.0f;
+    for (int c = wave; c < chunks; c += kWavesPerWG) {
+        const float mc = staged[c * kRow + kHeadDim];
+        if (mc == -INFINITY) continue;
+        const float f = fast_exp2(mc - M);
+        O = fmaf(staged[c * kRow + lane], f, O);
+        L = fmaf(staged[c * kRow + kHeadDim + 1], f, L);
+    }
+    red_o[wave][lane] = O;
+    if (lane == 0) red_l[wave] = L;
+    __syncthreads();
+    if (wave == 0) {
+        float o = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWavesPerWG; ++w) {
+            o += red_o[w][lane];
+            l += red_l[w];
+        }
+        out[h * kHeadDim + lane] = o / l;
+    }
 }
 
 __global__ void __launch_bounds__(kThreads) linear576_residual_kernel(const float* x, const float* w, const float* residual,
@@ -1463,6 +1423,10 @@ __global__ void __launch_bounds__(kThreads) lm_head_partial_kernel(const float* 
     const int64_t per = (vocab + TW - 1) / TW;
     const int64_t row0 = per * gw < vocab ? per * gw : vocab;
     const int64_t row1 = row0 + per < vocab ? row0 + per : vocab;
+    // The first rows are requested before the hidden vector, and each stage's successor
+    // before its dot products (lm_rows_pipelined), so the rows stream while a wave computes.
+    float wl[kLmBatch][9];
+    lm_load(lm_head, row0, row1, lane, wl);
     float h[9], x[9];
     fetch_slice576(PlainIn{hidden}, lane, h);
     if (norm_w != nullptr) {
@@ -1473,7 +1437,7 @@ __global__ void __launch_bounds__(kThreads) lm_head_partial_kernel(const float* 
     }
     float best_v = -INFINITY;
     int64_t best_i = INT64_MAX;
-    lm_rows(lm_head, x, row0, row1, lane, LogitsPlainOut{logits}, best_v, best_i);
+    lm_rows_pipelined(lm_head, x, wl, row0, row1, lane, LogitsPlainOut{logits}, best_v, best_i);
     wg_argmax(best_v, best_i, red_v, red_i);
     if (tid_opaque() == 0) {
         part_v[blockIdx.x] = best_v;
@@ -1652,7 +1616,8 @@ hipError_t launch_gqa_decode(const float* q, const float* key_cache, const float
                        q, key_cache, value_cache, position, capacity, scale, chunks, partials);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(kQHeads), dim3(kThreads), 0, stream, partials, chunks, out);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(kQHeads), dim3(kThreads),
+                       static_cast<size_t>(chunks) * (kHeadDim + 2) * sizeof(float), stream, partials, chunks, out);
     return hipGetLastError();
 }
 

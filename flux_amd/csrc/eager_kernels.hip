@@ -778,6 +778,19 @@ __global__ void __launch_bounds__(256) gqa_strided_merge_kernel(const float* __r
     const int h = blockIdx.x;
     const int64_t stride = dim + 2;
     const float* parts = workspace + static_cast<int64_t>(h) * chunks * stride;
+    // head_dim 64 with at most 64 chunks (contexts up to 8192): the chunk values this thread
+    // sums are requested together with the (m, l) words, so the block waits for one memory
+    // round trip instead of two.
+    constexpr int kPre = 16;
+    const bool pre = dim == 64 && chunks <= 4 * kPre;
+    float pv[kPre];
+    if (pre) {
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int c = wave + 4 * k;
+            pv[k] = c < chunks ? parts[c * stride + lane] : 0.0f;
+        }
+    }
     const float m = t < chunks ? parts[t * stride + dim] : -FLT_MAX;
     const float l = t < chunks ? parts[t * stride + dim + 1] : 0.0f;
     float mx = wave_max(m);
@@ -790,6 +803,18 @@ __global__ void __launch_bounds__(256) gqa_strided_merge_kernel(const float* __r
     if (lane == 0) stat[4 + wave] = total;
     __syncthreads();
     total = (stat[4] + stat[5]) + (stat[6] + stat[7]);
+    if (pre) {
+        float o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int c = wave + 4 * k;
+            if (c < chunks) o = fmaf(pv[k], weight[c], o);
+        }
+        red[wave * 64 + lane] = o;
+        __syncthreads();
+        if (wave == 0) out[h * 64 + lane] = ((red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane])) / total;
+        return;
+    }
     for (int d0 = 0; d0 < dim; d0 += 64) {
         const int d = d0 + lane;
         float o = 0.0f;

@@ -190,6 +190,30 @@ def test_config1_tokens_and_logits(smol_model):
     assert runtime.device_error() == 0
 
 
+def test_config1_whole_cache_against_oracle(smol_model):
+    """The SmolLM2-vocab model's whole K/V cache, not slices: after the config-1 prompt and
+    one generate_greedy(32) call, every layer's K and V at all 159 written positions equal
+    the CPU oracle's cache after the same greedy stream (the oracle is pinned to HF's
+    tokens, logits and K/V slices by the committed goldens)."""
+    record = golden("config1.npz")
+    n = len(record["tokens"])
+    prompt = torch.from_numpy(record["prompt"]).unsqueeze(0)
+    runtime = _capture(smol_model, record, n - 1)
+    generated = runtime.generate_greedy(n).clone()
+    torch.cuda.synchronize()
+    assert generated[0].cpu().numpy().tolist() == record["tokens"].tolist()
+    oracle = OracleLlama(synthetic.synthetic_state_dict(synthetic.SyntheticSpec(seed=0)))
+    tokens, _, cache = oracle.greedy(prompt, n)
+    assert tokens == record["tokens"].tolist()
+    written = prompt.shape[1] + n - 1
+    for layer in range(30):
+        torch.testing.assert_close(runtime.key_cache[layer, :, :, :written].float().cpu(),
+                                   cache.keys[layer][:, :, :written], rtol=KV_RTOL, atol=KV_ATOL)
+        torch.testing.assert_close(runtime.value_cache[layer, :, :, :written].float().cpu(),
+                                   cache.values[layer][:, :, :written], rtol=KV_RTOL, atol=KV_ATOL)
+    assert runtime.device_error() == 0
+
+
 @pytest.mark.parametrize("name", ["teacher_config1", "teacher_ctx8192"])
 def test_teacher_forced_changing_tokens(smol_model, name):
     """replay(token) with a seeded token sequence that changes at every step (48 steps after the
