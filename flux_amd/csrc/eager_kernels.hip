@@ -680,21 +680,26 @@ __global__ void __launch_bounds__(256) gqa_strided_chunk64_kernel(GqaStridedArgs
 
     const float* kbase = a.k + kh * a.k_strides[1] + begin * a.k_strides[2];
     const float* vbase = a.v + kh * a.v_strides[1] + begin * a.v_strides[2];
+    // Every load the block needs (q, its K and V rows and their mask values) is issued before
+    // any arithmetic, so the block waits for one memory round trip.
+    const float* qrow = a.q + h * a.q_strides[1];
+    const float4 q4 = make_float4(qrow[d0 * a.q_strides[3]], qrow[(d0 + 1) * a.q_strides[3]],
+                                  qrow[(d0 + 2) * a.q_strides[3]], qrow[(d0 + 3) * a.q_strides[3]]);
     float4 kv[kGqa64Keys], vv[kGqa64Keys];
+    float mk[kGqa64Keys];
 #pragma unroll
     for (int i = 0; i < kGqa64Keys; ++i) {
         const int j = slot + 16 * i;
+        mk[i] = 0.0f;
         if (j < n) {
             kv[i] = load_row4<kVec>(kbase + j * a.k_strides[2], a.k_strides[3], d0);
             vv[i] = load_row4<kVec>(vbase + j * a.v_strides[2], a.v_strides[3], d0);
+            if (a.mask != nullptr) mk[i] = a.mask[h * a.mask_strides[1] + (begin + j) * a.mask_strides[3]];
         } else {
             kv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             vv[i] = kv[i];
         }
     }
-    const float* qrow = a.q + h * a.q_strides[1];
-    const float4 q4 = make_float4(qrow[d0 * a.q_strides[3]], qrow[(d0 + 1) * a.q_strides[3]],
-                                  qrow[(d0 + 2) * a.q_strides[3]], qrow[(d0 + 3) * a.q_strides[3]]);
 
     float score[kGqa64Keys];
     float mx = -FLT_MAX;
@@ -710,7 +715,7 @@ __global__ void __launch_bounds__(256) gqa_strided_chunk64_kernel(GqaStridedArgs
         if (j < n) {
 #pragma clang fp contract(off)
             sc = dot * a.scale;
-            if (a.mask != nullptr) sc = sc + a.mask[h * a.mask_strides[1] + (begin + j) * a.mask_strides[3]];
+            if (a.mask != nullptr) sc = sc + mk[i];
         }
         score[i] = sc;
         mx = fmaxf(mx, sc);
