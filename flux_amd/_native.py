@@ -147,7 +147,7 @@ _PROTOTYPES: list[tuple[str, Any, list[Any]]] = [
     ("flux_layer_decode_replay_count", ctypes.c_int, [_vp, _i64]),
     ("flux_layer_decode_capacity", ctypes.c_int, [_vp, _i64]),
     ("flux_layer_decode_get_buffers", ctypes.c_int, [_vp, ctypes.POINTER(LayerDecodeBuffers)]),
-    ("flux_layer_decode_graph_nodes", ctypes.c_int, [_vp, _i64, _i64]),
+    ("flux_layer_decode_replay_launches", ctypes.c_int, [_vp, _i64, _i64]),
     ("flux_layer_decode_destroy", None, [_vp]),
     ("flux_rmsnorm_f32", ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, _stream]),
     ("flux_residual_rmsnorm_f32", ctypes.c_int,

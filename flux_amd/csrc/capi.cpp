@@ -502,10 +502,12 @@ int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_d
     return FLUX_OK;
 }
 
-int flux_layer_decode_graph_nodes(const flux_layer_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes) {
-    if (runtime == nullptr || kernel_nodes == nullptr || total_nodes == nullptr)
-        return invalid("flux_layer_decode_graph_nodes: null argument");
-    return guarded([&] { runtime->impl->graph_nodes(kernel_nodes, total_nodes); });
+int flux_layer_decode_replay_launches(const flux_layer_decode* runtime, int64_t* kernel_launches,
+                                     int64_t* device_commands) {
+    if (runtime == nullptr || kernel_launches == nullptr || device_commands == nullptr)
+        return invalid("flux_layer_decode_replay_launches: null argument");
+    runtime->impl->replay_launches(kernel_launches, device_commands);
+    return FLUX_OK;
 }
 
 void flux_layer_decode_destroy(flux_layer_decode* runtime) {

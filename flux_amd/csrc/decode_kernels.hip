@@ -877,7 +877,10 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         abort_flag = 0;
         wait_shared = WaitShared{args.host_error, args.wait_ticks};
     }
-    if (tid_opaque() < kLayers) layer_desc[tid_opaque()] = args.layers[tid_opaque()];
+    // Layers per step: kLayers for the token loop, 1 for the single-layer step
+    // (NativeSmolLM2LayerDecode), whose descriptor array holds that layer only.
+    const int n_layers = wave_uniform(args.layer_count);
+    if (static_cast<int>(tid_opaque()) < n_layers) layer_desc[tid_opaque()] = args.layers[tid_opaque()];
     const uint32_t counter0 = *args.token_counter;
     // The token state is the same for every lane: kept in scalar registers.
     auto uniform64 = [](int64_t v) {
@@ -916,7 +919,7 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
         const int tchunks_token = __builtin_amdgcn_readfirstlane(want_chunks < chunks ? want_chunks : chunks);
         const float* emb_row = args.embedding + (token_ok ? token : 0) * kHidden;
 
-        for (int layer = 0; layer < kLayers; ++layer) {
+        for (int layer = 0; layer < n_layers; ++layer) {
             int tchunks = tchunks_token;
             asm volatile("" : "+s"(tchunks));
             const LayerWeights Lw = uniform_desc(layer_desc[layer]);
@@ -938,7 +941,15 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                     load_slice576(Lw.input_norm, lane, wn);
                     rp = rope_pair(cos_row, sin_row, gw);
                 }
-                if (layer == 0) {
+                if (layer == 0 && args.hidden_in != nullptr) {
+                    // Single-layer step: the caller's hidden state (workgroup 0 also keeps a copy
+                    // in hidden_save, the input of a later step that passes none).
+                    for (int k = tid_opaque(); k < kHidden; k += kThreads) {
+                        const float v = args.hidden_in[k];
+                        hvec[k] = v;
+                        if (wg == 0 && args.hidden_save != nullptr) args.hidden_save[k] = v;
+                    }
+                } else if (layer == 0) {
                     for (int k = tid_opaque(); k < kHidden; k += kThreads) hvec[k] = token_ok ? emb_row[k] : 0.0f;
                 } else {
                     wg_ll_fetch<2>(ll_prev + replica + LLLayout::kHidden, kHidden, Contiguous{}, epoch_of(counter, layer - 1),
@@ -1149,6 +1160,24 @@ __global__ void __launch_bounds__(kThreads, 1) fused_decode_kernel(DecodeArgs ar
                 }
                 __syncthreads();
             }
+        }
+
+        if (args.hidden_out != nullptr) {
+            // Single-layer step: workgroup 0 gathers the layer's output h into hidden_out and
+            // advances the position; there is no LM head.  The step's K/V rows were written
+            // through (agent-scope stores), so the next launch reads them from memory.
+            if (wg == 0) {
+                wg_ll_fetch<2>(args.ll + ((n_layers - 1) & 1) * LLLayout::kParity + replica + LLLayout::kHidden,
+                               kHidden, Contiguous{}, epoch_of(counter, n_layers - 1), wctx, hvec);
+                __syncthreads();
+                for (int k = tid_opaque(); k < kHidden; k += kThreads) args.hidden_out[k] = hvec[k];
+                if (tid_opaque() == 0) {
+                    *args.position = attended;
+                    *args.cache_length = attended;
+                }
+            }
+            position = attended;
+            continue;
         }
 
         // ---- final norm -> LM head -> argmax ----

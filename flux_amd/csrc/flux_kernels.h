@@ -39,6 +39,16 @@ struct DecodeArgs {
     // When set, the launch's first step reads its input token here instead of from
     // input_token (replay(token): the caller's token, read in stream order, no copy).
     const int64_t* token_in;
+    // Layers per step: kLayers, or 1 for the single-layer step of NativeSmolLM2LayerDecode
+    // (layers then holds that layer only, and the caches are its [3, capacity, 64]).
+    int layer_count;
+    // Single-layer step (hidden_out set): the step starts from hidden_in instead of the
+    // token's embedding row (workgroup 0 copies it to hidden_save when that is set), writes
+    // the last layer's output to hidden_out and advances *position and *cache_length by
+    // one; no LM head, no argmax, no generation bookkeeping.
+    const float* hidden_in;
+    float* hidden_save;
+    float* hidden_out;
 };
 
 // ---- fused decode ----

@@ -97,22 +97,6 @@ hipError_t counted_memcpy(void* dst, const void* src, size_t bytes, hipMemcpyKin
     return hipMemcpy(dst, src, bytes, kind);
 }
 
-// Kernel nodes and all nodes of an instantiated step graph.
-void count_graph_nodes(hipGraph_t graph, int64_t* kernels, int64_t* total) {
-    size_t count = 0;
-    check_hip(hipGraphGetNodes(graph, nullptr, &count), "counting graph nodes");
-    std::vector<hipGraphNode_t> nodes(count);
-    if (count > 0) check_hip(hipGraphGetNodes(graph, nodes.data(), &count), "listing graph nodes");
-    int64_t k = 0;
-    for (hipGraphNode_t node : nodes) {
-        hipGraphNodeType type;
-        check_hip(hipGraphNodeGetType(node, &type), "reading graph node type");
-        if (type == hipGraphNodeTypeKernel) ++k;
-    }
-    *kernels = k;
-    *total = static_cast<int64_t>(count);
-}
-
 [[noreturn]] void invalid(const std::string& message) { throw FluxError(FLUX_ERROR_INVALID_VALUE, message); }
 [[noreturn]] void bad_state(const std::string& message) { throw FluxError(FLUX_ERROR_STATE, message); }
 
@@ -181,10 +165,6 @@ void DecodeRuntime::replay_launches(int64_t* kernels, int64_t* commands) const {
     *commands = replay_commands_;
 }
 
-void LayerDecodeRuntime::graph_nodes(int64_t* kernels, int64_t* total) const {
-    count_graph_nodes(graph_, kernels, total);
-}
-
 int isolated_attention_chunks(int64_t capacity) {
     int chunks = 85;
     while (gqa_decode_max_positions(chunks) < capacity) chunks *= 2;
@@ -236,7 +216,8 @@ DecodeRuntime::DecodeRuntime(const flux_weights& weights, const float* rope_cos,
         args_ = DecodeArgs{layers_, weights.embedding, weights.lm_head, weights.final_norm, final_eps_,
                            rope_cos_, rope_sin_, key_cache_, value_cache_, logits_, input_token_, generated_,
                            generation_step_, position_, cache_length_, ll_, token_counter_, error_,
-                           host_error_device_, kDefaultWaitTicks, capacity_, vocab_, capacity_, 1, nullptr};
+                           host_error_device_, kDefaultWaitTicks, capacity_, vocab_, capacity_, 1, nullptr,
+                           kLayers, nullptr, nullptr, nullptr};
 
         check_hip(hipEventCreateWithFlags(&completion_, hipEventDisableTiming), "creating completion event");
 
@@ -781,12 +762,12 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
     if (rope_cos == nullptr || rope_sin == nullptr) invalid("flux native decode: RoPE tables are required");
     validate_state(initial_hidden, key_source, value_source, source_length, position);
     check_hip(hipGetDevice(&device_), "hipGetDevice");
-    grid_ = device_cu_count();
-    chunks_ = isolated_attention_chunks(capacity_);
+    grid_ = decode_grid();
+    if (capacity_ > max_attention_positions(grid_))
+        invalid("flux native decode: capacity exceeds what the fused attention split can hold on this device");
 
     try {
         const size_t cache_elems = static_cast<size_t>(kKVHeads) * capacity_ * kHeadDim;
-        const size_t partial_floats = static_cast<size_t>(chunks_) * kKVHeads * kGroup * (kHeadDim + 2);
         size_t offset = 0;
         auto take = [&](size_t bytes) {
             const size_t at = offset;
@@ -798,13 +779,13 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
         const size_t o_key = take(cache_elems * sizeof(float));
         const size_t o_value = take(cache_elems * sizeof(float));
         const size_t o_position = take(sizeof(int64_t));
-        const size_t o_query = take(kQHeads * kHeadDim * sizeof(float));
-        const size_t o_attention = take(kHidden * sizeof(float));
-        const size_t o_residual = take(kHidden * sizeof(float));
-        const size_t o_swiglu = take(kInter * sizeof(float));
-        const size_t o_partials = take(partial_floats * sizeof(float));
+        const size_t o_length = take(sizeof(int64_t));
+        const size_t o_token = take(sizeof(int64_t));
+        const size_t o_step = take(sizeof(int64_t));
+        const size_t o_counter = take(sizeof(uint32_t));
+        const size_t o_error = take(sizeof(int32_t));
+        const size_t o_layers = take(sizeof(LayerWeights));
         block_bytes_ = offset;
-        workspace_bytes_ = offset - o_query;
         check_hip(counted_malloc(&block_, block_bytes_), "allocating layer decode buffers");
         char* base = static_cast<char*>(block_);
         input_hidden_ = reinterpret_cast<float*>(base + o_hidden);
@@ -812,40 +793,42 @@ LayerDecodeRuntime::LayerDecodeRuntime(const LayerWeights& layer, const float* r
         key_cache_ = reinterpret_cast<float*>(base + o_key);
         value_cache_ = reinterpret_cast<float*>(base + o_value);
         position_ = reinterpret_cast<int64_t*>(base + o_position);
-        workspace_ = reinterpret_cast<float*>(base + o_query);
-        query_ = reinterpret_cast<float*>(base + o_query);
-        attention_ = reinterpret_cast<float*>(base + o_attention);
-        residual_ = reinterpret_cast<float*>(base + o_residual);
-        swiglu_ = reinterpret_cast<float*>(base + o_swiglu);
-        partials_ = reinterpret_cast<float*>(base + o_partials);
-
-        check_hip(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking), "creating capture stream");
+        cache_length_ = reinterpret_cast<int64_t*>(base + o_length);
+        token_word_ = reinterpret_cast<int64_t*>(base + o_token);
+        step_word_ = reinterpret_cast<int64_t*>(base + o_step);
+        token_counter_ = reinterpret_cast<uint32_t*>(base + o_counter);
+        error_ = reinterpret_cast<int32_t*>(base + o_error);
+        layers_ = reinterpret_cast<LayerWeights*>(base + o_layers);
+        ll_bytes_ = ll_arena_words() * sizeof(uint64_t);
+        check_hip(arena_pool().acquire(device_, ll_bytes_, &ll_), "allocating the uncached exchange arena");
+        check_hip(hipHostMalloc(reinterpret_cast<void**>(&host_error_), sizeof(int32_t),
+                                hipHostMallocMapped | hipHostMallocCoherent),
+                  "allocating the host-visible error word");
+        *host_error_ = 0;
+        check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&host_error_device_), host_error_, 0),
+                  "mapping the host-visible error word");
         check_hip(hipEventCreateWithFlags(&completion_, hipEventDisableTiming), "creating completion event");
 
-        // Warm one step (as the reference does before capture), then restore the state.
-        initialize_state(initial_hidden, key_source, value_source, source_length, position, stream, false);
-        hipEvent_t setup = nullptr;
-        check_hip(hipEventCreateWithFlags(&setup, hipEventDisableTiming), "creating setup event");
-        check_hip(hipEventRecord(setup, stream), "recording setup event");
-        check_hip(hipStreamWaitEvent(capture_stream_, setup, 0), "ordering setup");
-        run_body(capture_stream_);
-        check_hip(counted_stream_sync(capture_stream_), "warming layer decode");
-        check_hip(hipEventDestroy(setup), "destroying setup event");
-        initialize_state(initial_hidden, key_source, value_source, source_length, position, capture_stream_, true);
-        check_hip(counted_stream_sync(capture_stream_), "initialising layer decode state");
+        check_hip(hipMemcpyAsync(layers_, &layer_, sizeof(LayerWeights), hipMemcpyHostToDevice, stream),
+                  "uploading layer descriptor");
+        check_hip(hipMemsetAsync(ll_, 0, ll_bytes_, stream), "clearing exchange arena");
+        check_hip(hipMemsetAsync(token_counter_, 0, sizeof(uint32_t), stream), "clearing token counter");
+        check_hip(hipMemsetAsync(token_word_, 0, sizeof(int64_t), stream), "clearing token word");
+        check_hip(hipMemsetAsync(step_word_, 0, sizeof(int64_t), stream), "clearing step word");
+        check_hip(hipMemsetAsync(error_, 0, sizeof(int32_t), stream), "clearing error word");
+        // The fused decode kernel in its single-layer mode: one layer, no token, no LM head.
+        args_ = DecodeArgs{layers_, nullptr, nullptr, nullptr, 0.0f, rope_cos_, rope_sin_, key_cache_, value_cache_,
+                           nullptr, token_word_, nullptr, step_word_, position_, cache_length_,
+                           static_cast<uint64_t*>(ll_), token_counter_, error_, host_error_device_, kDefaultWaitTicks,
+                           capacity_, 1, 0, 1, nullptr, 1, input_hidden_, nullptr, output_};
 
-        check_hip(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal), "beginning graph capture");
-        try {
-            run_body(capture_stream_);
-        } catch (...) {
-            hipGraph_t abandoned = nullptr;
-            (void)hipStreamEndCapture(capture_stream_, &abandoned);
-            if (abandoned) (void)hipGraphDestroy(abandoned);
-            throw;
-        }
-        check_hip(hipStreamEndCapture(capture_stream_, &graph_), "ending graph capture");
-        check_hip(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0), "instantiating layer graph");
-        check_hip(counted_stream_sync(capture_stream_), "finalising capture");
+        // Warm one step, then restore the state (the reference warms the step before capture).
+        initialize_state(initial_hidden, key_source, value_source, source_length, position, stream, false);
+        check_hip(launch_fused_decode(args_, grid_, stream, false), "warming layer decode");
+        check_hip(counted_stream_sync(stream), "warming layer decode");
+        check_host_error();
+        initialize_state(initial_hidden, key_source, value_source, source_length, position, stream, true);
+        check_hip(counted_stream_sync(stream), "initialising layer decode state");
     } catch (...) {
         release();
         throw;
@@ -859,20 +842,20 @@ void LayerDecodeRuntime::release() noexcept {
     (void)hipGetDevice(&previous);
     (void)hipSetDevice(device_);
     if (pending_ && completion_ != nullptr) (void)counted_event_sync(completion_);
-    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-    if (graph_) (void)hipGraphDestroy(graph_);
     if (completion_) (void)hipEventDestroy(completion_);
-    if (capture_stream_) {
-        (void)counted_stream_sync(capture_stream_);
-        (void)hipStreamDestroy(capture_stream_);
-    }
     if (block_) (void)counted_free(block_);
-    graph_exec_ = nullptr;
-    graph_ = nullptr;
+    if (ll_) arena_pool().release(device_, ll_bytes_, ll_);
+    if (host_error_) (void)hipHostFree(host_error_);
     completion_ = nullptr;
-    capture_stream_ = nullptr;
     block_ = nullptr;
+    ll_ = nullptr;
+    host_error_ = host_error_device_ = nullptr;
     if (previous >= 0 && previous != device_) (void)hipSetDevice(previous);
+}
+
+void LayerDecodeRuntime::check_host_error() const {
+    const int32_t err = __atomic_load_n(host_error_, __ATOMIC_ACQUIRE);
+    if (err != 0) throw FluxError(FLUX_ERROR_DEVICE, device_error_message(err));
 }
 
 void LayerDecodeRuntime::validate_state(const float* hidden, const float* key_source, const float* value_source,
@@ -907,37 +890,36 @@ void LayerDecodeRuntime::initialize_state(const float* hidden, const float* key_
     staged_position_ = position;
     check_hip(hipMemcpyAsync(position_, &staged_position_, sizeof(int64_t), hipMemcpyHostToDevice, stream),
               "initialising device position");
+    check_hip(hipMemcpyAsync(cache_length_, &staged_position_, sizeof(int64_t), hipMemcpyHostToDevice, stream),
+              "initialising device cache length");
     if (clear_output) check_hip(hipMemsetAsync(output_, 0, kHidden * sizeof(float), stream), "clearing layer output");
 }
 
-// The step, as native_decode_runtime_cuda.cu:192-310 orders it: RMSNorm + packed QKV
-// GEMV + RoPE + cache row at *position; GQA over [0, *position]; o_proj + residual;
-// RMSNorm + gate/up GEMV + SwiGLU; down + residual; then *position += 1.
-void LayerDecodeRuntime::run_body(hipStream_t stream) {
-    check_hip(launch_qkv_rope_cache(input_hidden_, layer_.input_norm, layer_.eps, layer_.qkv, rope_cos_, rope_sin_,
-                                    position_, capacity_, key_cache_, value_cache_, query_, grid_, stream),
-              "launching QKV/RoPE/cache step");
-    check_hip(launch_gqa_decode(query_, key_cache_, value_cache_, position_, capacity_, layer_.scale, chunks_,
-                                partials_, attention_, stream),
-              "launching GQA decode attention");
-    check_hip(launch_linear576_residual(attention_, layer_.o_proj, input_hidden_, residual_, kHidden, grid_, stream),
-              "launching attention output projection");
-    check_hip(launch_gate_up_swiglu(residual_, layer_.post_norm, layer_.eps, layer_.gate_up, swiglu_, grid_, stream),
-              "launching gate/up SwiGLU");
-    check_hip(launch_down_residual(swiglu_, layer_.down, residual_, output_, grid_, stream),
-              "launching down projection");
-    check_hip(launch_advance_position(position_, stream), "advancing position");
-}
-
+// The step, as native_decode_runtime_cuda.cu:192-310 orders it: RMSNorm + packed QKV GEMV + RoPE
+// + cache row at *position; GQA over [0, *position]; o_proj + residual; RMSNorm + gate/up GEMV +
+// SwiGLU; down + residual; then *position += 1.  One plain launch of the fused decode kernel in
+// its single-layer mode: it reads the caller's hidden state directly (workgroup 0 keeps a copy
+// as the input of a later replay that passes none), so there is no copy; the caller's buffer
+// must hold its value until the step has run (stream order).  Every workgroup fits the device
+// at once (occupancy is checked at creation) and every cross-workgroup wait is bounded.
 float* LayerDecodeRuntime::replay(const float* hidden, hipStream_t stream) {
     if (replay_count_ >= capacity_ - start_position_) bad_state("flux native decode: fixed-capacity state is exhausted");
     check_hip(hipSetDevice(device_), "hipSetDevice");
-    if (pending_) check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering consecutive replays");
-    if (hidden != nullptr)
-        check_hip(hipMemcpyAsync(input_hidden_, hidden, kHidden * sizeof(float), hipMemcpyDeviceToDevice, stream),
-                  "copying replay hidden state");
-    check_hip(hipGraphLaunch(graph_exec_, stream), "launching layer graph");
+    check_host_error();
+    if (pending_ && stream != last_stream_) {
+        check_hip(hipStreamWaitEvent(stream, completion_, 0), "ordering consecutive replays");
+        ++replay_commands_;
+    }
+    DecodeArgs args = args_;
+    if (hidden != nullptr) {
+        args.hidden_in = hidden;
+        args.hidden_save = input_hidden_;
+    }
+    check_hip(launch_fused_decode(args, grid_, stream, false), "launching layer step");
+    ++replay_kernels_;
+    ++replay_commands_;
     check_hip(hipEventRecord(completion_, stream), "recording replay completion");
+    last_stream_ = stream;
     pending_ = true;
     ++replay_count_;
     return output_;
@@ -952,7 +934,9 @@ void LayerDecodeRuntime::reset(const float* hidden, const float* key_source, con
         pending_ = false;
     }
     initialize_state(hidden, key_source, value_source, source_length, position, stream, true);
+    check_hip(hipMemsetAsync(error_, 0, sizeof(int32_t), stream), "clearing error word");
     check_hip(counted_stream_sync(stream), "resetting runtime state");
+    *host_error_ = 0;
     start_position_ = position;
     replay_count_ = 0;
 }
@@ -960,25 +944,27 @@ void LayerDecodeRuntime::reset(const float* hidden, const float* key_source, con
 int64_t LayerDecodeRuntime::position() {
     check_hip(hipSetDevice(device_), "hipSetDevice");
     if (pending_) check_hip(counted_event_sync(completion_), "waiting to inspect device position");
+    check_host_error();
     int64_t result = -1;
     check_hip(counted_memcpy(&result, position_, sizeof(result), hipMemcpyDeviceToHost), "reading device position");
     return result;
 }
 
+void LayerDecodeRuntime::replay_launches(int64_t* kernels, int64_t* commands) const {
+    *kernels = replay_kernels_;
+    *commands = replay_commands_;
+}
+
 void LayerDecodeRuntime::buffers(flux_layer_decode_buffers* out) const {
+    std::memset(out, 0, sizeof(*out));
     out->input_hidden = input_hidden_;
     out->output = output_;
     out->key_cache = key_cache_;
     out->value_cache = value_cache_;
     out->position = position_;
-    out->workspace = workspace_;
-    out->query = query_;
-    out->attention = attention_;
-    out->residual = residual_;
-    out->swiglu = swiglu_;
-    out->attention_partials = partials_;
+    out->workspace = ll_;
     out->capacity = capacity_;
-    out->workspace_bytes = static_cast<int64_t>(workspace_bytes_);
+    out->workspace_bytes = static_cast<int64_t>(ll_bytes_);
 }
 
 }  // namespace flux

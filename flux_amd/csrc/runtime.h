@@ -167,9 +167,10 @@ private:
     int lm_grid_ = 0;
 };
 
-// One decoder layer's token step captured in a hipGraph: input hidden [576] ->
-// output hidden [576], with the layer's own compact cache [1, 3, capacity, 64]
-// and device position (advanced by every replay).
+// One decoder layer's token step: input hidden [576] -> output hidden [576], with the
+// layer's own compact cache [1, 3, capacity, 64] and device position (advanced by every
+// replay).  A replay is one launch of the fused decode kernel in its single-layer mode
+// (the layer's phases exchange through an uncached arena, as the token loop's do).
 class LayerDecodeRuntime {
 public:
     LayerDecodeRuntime(const LayerWeights& layer, const float* rope_cos, const float* rope_sin, int64_t capacity,
@@ -186,47 +187,52 @@ public:
     int64_t replay_count() const { return replay_count_; }
     int64_t capacity() const { return capacity_; }
     void buffers(flux_layer_decode_buffers* out) const;
-    void graph_nodes(int64_t* kernels, int64_t* total) const;
+    // Kernel launches and all device commands (launches, event waits) issued by replay()
+    // since creation.
+    void replay_launches(int64_t* kernels, int64_t* commands) const;
 
 private:
     void validate_state(const float* hidden, const float* key_source, const float* value_source,
                         int64_t source_length, int64_t position) const;
     void initialize_state(const float* hidden, const float* key_source, const float* value_source,
                           int64_t source_length, int64_t position, hipStream_t stream, bool clear_output);
-    void run_body(hipStream_t stream);
+    // Raises FluxError(FLUX_ERROR_DEVICE) when a finished launch reported a device-side error.
+    void check_host_error() const;
     void release() noexcept;
 
     int device_ = 0;
     int grid_ = 0;
-    int chunks_ = 0;
     int64_t capacity_ = 0;
     int64_t start_position_ = 0;
     int64_t replay_count_ = 0;
     int64_t staged_position_ = 0;
+    int64_t replay_kernels_ = 0;
+    int64_t replay_commands_ = 0;
     bool pending_ = false;
+    hipStream_t last_stream_ = nullptr;
     LayerWeights layer_{};
     const float* rope_cos_ = nullptr;
     const float* rope_sin_ = nullptr;
 
     void* block_ = nullptr;
     size_t block_bytes_ = 0;
-    size_t workspace_bytes_ = 0;
     float* input_hidden_ = nullptr;   // [576]
     float* output_ = nullptr;         // [576]
     float* key_cache_ = nullptr;      // [3, capacity, 64]
     float* value_cache_ = nullptr;
     int64_t* position_ = nullptr;
-    float* workspace_ = nullptr;      // query | attention | residual | swiglu | attention partials
-    float* query_ = nullptr;          // [9, 64]
-    float* attention_ = nullptr;      // [576]
-    float* residual_ = nullptr;       // [576] input + o_proj(attention)
-    float* swiglu_ = nullptr;         // [1536]
-    float* partials_ = nullptr;       // split-key attention partials
-
-    hipStream_t capture_stream_ = nullptr;
+    int64_t* cache_length_ = nullptr;
+    int64_t* token_word_ = nullptr;   // the kernel's token and step words (unused by the layer step)
+    int64_t* step_word_ = nullptr;
+    uint32_t* token_counter_ = nullptr;
+    int32_t* error_ = nullptr;
+    LayerWeights* layers_ = nullptr;  // device copy of layer_
+    void* ll_ = nullptr;              // exchange arena (uncached pool)
+    size_t ll_bytes_ = 0;
+    int32_t* host_error_ = nullptr;         // mapped pinned host memory
+    int32_t* host_error_device_ = nullptr;  // its device address
     hipEvent_t completion_ = nullptr;
-    hipGraph_t graph_ = nullptr;
-    hipGraphExec_t graph_exec_ = nullptr;
+    DecodeArgs args_{};
 };
 
 int device_cu_count();

@@ -696,15 +696,18 @@ _LAYER_ADDRESS_NAMES = ("input_hidden", "output", "key_cache", "value_cache", "d
 
 
 class NativeSmolLM2LayerDecode:
-    """One SmolLM2 decoder layer's token step as a replayable native graph.
+    """One SmolLM2 decoder layer's token step as a replayable native step.
 
     Mirror of ``torch.classes.flux.NativeSmolLM2LayerDecode``
     (``csrc/native_decode_runtime/native_decode_runtime.h:13-54``, registered in
     ``native_decode_runtime_torch.cpp:5-36``): the constructor arguments, methods
-    and validation messages are the reference's; the step runs this build's
-    decode kernels (RMSNorm + packed QKV GEMV + RoPE + cache row, GQA decode,
-    o_proj + residual, RMSNorm + gate/up SwiGLU, down + residual) and advances
-    the device position.  ``replay`` returns the stable ``[1, 1, 576]`` output.
+    and validation messages are the reference's.  A step (RMSNorm + packed QKV GEMV
+    + RoPE + cache row, GQA decode, o_proj + residual, RMSNorm + gate/up SwiGLU,
+    down + residual, position advance) is one launch of the fused decode kernel in
+    its single-layer mode, where the reference replays a CUDA graph of the step's
+    kernels.  ``replay`` returns the stable ``[1, 1, 576]`` output.  The step's
+    intermediates are exchanged through the workspace arena, so their addresses
+    (query, attention, residual, swiglu, attention partials) are 0.
     """
 
     def __init__(self, initial_hidden: torch.Tensor, input_norm_weight: torch.Tensor,
@@ -783,7 +786,8 @@ class NativeSmolLM2LayerDecode:
                                "tensors shaped [1, 3, sequence>=position, 64]")
 
     def replay(self, hidden: torch.Tensor | None = None) -> torch.Tensor:
-        """Enqueue an optional hidden copy and one graph launch; returns the output buffer."""
+        """Enqueue one step launch (it reads ``hidden``, or the last input when None, in
+        stream order and keeps it as the input); returns the output buffer."""
         if hidden is not None:
             _check_layer_tensor(hidden, self._device, (1, 1, 576), "replay hidden state")
         with torch.cuda.device(self._device):
@@ -842,12 +846,12 @@ class NativeSmolLM2LayerDecode:
     def workspace_bytes(self) -> int:
         return int(self._buffers.workspace_bytes)
 
-    def graph_nodes(self) -> tuple[int, int]:
-        """(kernel nodes, all nodes) of the captured layer-step graph."""
-        kernels, total = ctypes.c_int64(), ctypes.c_int64()
-        _native.check(_native.load().flux_layer_decode_graph_nodes(self._raw, ctypes.byref(kernels),
-                                                                   ctypes.byref(total)))
-        return int(kernels.value), int(total.value)
+    def replay_launches(self) -> tuple[int, int]:
+        """(kernel launches, all device commands) that replay() has issued since creation."""
+        kernels, commands = ctypes.c_int64(), ctypes.c_int64()
+        _native.check(_native.load().flux_layer_decode_replay_launches(self._raw, ctypes.byref(kernels),
+                                                                       ctypes.byref(commands)))
+        return int(kernels.value), int(commands.value)
 
 
 

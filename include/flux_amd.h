@@ -222,10 +222,13 @@ void flux_prefill_destroy(flux_prefill* runtime);
  *  native_decode_runtime_cuda.cu:314-738,1340-1400; registered in
  *  native_decode_runtime_torch.cpp:5-36).
  * One decoder layer's token step (input hidden [1,1,576] -> output [1,1,576]) with
- * its own K/V cache [1,3,capacity,64] and device position, captured in a hipGraph.
- * key_source/value_source: [1,3,source_length,64] contiguous, source_length >= position
- * (may be NULL when position == 0).  Each replay writes K/V row *position, attends
- * [0, *position] and advances the position. */
+ * its own K/V cache [1,3,capacity,64] and device position.  A step is one launch of the
+ * fused decode kernel in its single-layer mode (the reference replays a CUDA graph of the
+ * step's kernels; the phases here exchange through an uncached arena, as the token
+ * loop's do).  key_source/value_source: [1,3,source_length,64] contiguous,
+ * source_length >= position (may be NULL when position == 0).  Each replay writes K/V
+ * row *position, attends [0, *position] and advances the position.  Needs the same
+ * device as flux_decode_create (every workgroup of a launch resident at once). */
 typedef struct flux_layer_weights {
     const float* input_norm; /* [576] */
     const float* packed_qkv; /* [960, 576] */
@@ -237,19 +240,21 @@ typedef struct flux_layer_weights {
 
 typedef struct flux_layer_decode flux_layer_decode;
 
-/* NativeSmolLM2LayerDecode::addresses() counterparts (native_decode_runtime_cuda.cu:1388-1406). */
+/* NativeSmolLM2LayerDecode::addresses() counterparts (native_decode_runtime_cuda.cu:1388-1406).
+ * The step's intermediates (query, attention, residual, SwiGLU, attention partials) are
+ * exchanged through the workspace arena and not kept as arrays: those fields are NULL. */
 typedef struct flux_layer_decode_buffers {
-    float* input_hidden;       /* [576] */
+    float* input_hidden;       /* [576]: the last replay's (or the initial) input */
     float* output;             /* [576] */
     float* key_cache;          /* [1, 3, capacity, 64] */
     float* value_cache;        /* [1, 3, capacity, 64] */
     int64_t* position;         /* [1] */
-    void* workspace;           /* the intermediates below, one block */
-    float* query;              /* [9, 64] */
-    float* attention;          /* [576] */
-    float* residual;           /* [576] */
-    float* swiglu;             /* [1536] */
-    float* attention_partials; /* split-key partials */
+    void* workspace;           /* exchange arena (uncached device memory) */
+    float* query;              /* NULL */
+    float* attention;          /* NULL */
+    float* residual;           /* NULL */
+    float* swiglu;             /* NULL */
+    float* attention_partials; /* NULL */
     int64_t capacity;
     int64_t workspace_bytes;
 } flux_layer_decode_buffers;
@@ -258,8 +263,9 @@ int flux_layer_decode_create(const flux_layer_weights* weights, const float* rop
                              int64_t capacity, int64_t position, const float* initial_hidden, const float* key_source,
                              const float* value_source, int64_t source_length, double epsilon,
                              double attention_scale, hipStream_t stream, flux_layer_decode** out);
-/* One step (optional hidden copy, then graph replay); returns the output buffer.
- * (native_decode_runtime_cuda.cu:456-481) */
+/* One step; returns the output buffer.  hidden (or NULL: the last input again) is read by
+ * the step itself, in stream order, and kept as input_hidden; it must hold its value until
+ * the step has run.  (native_decode_runtime_cuda.cu:456-481) */
 int flux_layer_decode_replay(flux_layer_decode* runtime, const float* hidden, hipStream_t stream, float** output);
 /* Synchronously restore hidden, cache and position.  (native_decode_runtime_cuda.cu:483-501) */
 int flux_layer_decode_reset(flux_layer_decode* runtime, const float* hidden, const float* key_source,
@@ -268,7 +274,11 @@ int flux_layer_decode_position(flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_replay_count(const flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_capacity(const flux_layer_decode* runtime, int64_t* out);
 int flux_layer_decode_get_buffers(const flux_layer_decode* runtime, flux_layer_decode_buffers* out);
-int flux_layer_decode_graph_nodes(const flux_layer_decode* runtime, int64_t* kernel_nodes, int64_t* total_nodes);
+/* Kernel launches and all device commands (launches, cross-stream event waits) that replay()
+ * has issued since creation: one launch per step.  Replaces the graph-node audit of the
+ * reference's captured step (native_decode_runtime_cuda.cu:456-481). */
+int flux_layer_decode_replay_launches(const flux_layer_decode* runtime, int64_t* kernel_launches,
+                                     int64_t* device_commands);
 void flux_layer_decode_destroy(flux_layer_decode* runtime);
 
 /* ------------------------------------------------------------------------ */

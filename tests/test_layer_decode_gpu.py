@@ -127,5 +127,5 @@ def test_layer_capacity_and_validation(layer_setup, gpu_device):
     runtime.reset(hidden, keys, keys.clone(), 3)
     assert runtime.position() == 3
     assert runtime.workspace_bytes() > 0 and runtime.workspace().numel() * 4 == runtime.workspace_bytes()
-    # QKV/RoPE/cache, attention partials, attention merge, o_proj, gate/up, down, position advance.
-    assert runtime.graph_nodes() == (7, 7)
+    # Every replay above was one launch of the fused kernel's single-layer step on one stream.
+    assert runtime.replay_launches() == (2, 2)
