@@ -834,19 +834,10 @@ __global__ void __launch_bounds__(256) gqa_strided_merge_kernel(const float* __r
     }
 }
 
-__global__ void advance_position_kernel(int64_t* position) {
-    if (threadIdx.x == 0) *position += 1;
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // Host launchers.
-
-hipError_t launch_advance_position(int64_t* position, hipStream_t stream) {
-    hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, stream, position);
-    return hipGetLastError();
-}
 
 hipError_t launch_rope(const float* query, const float* key, const float* cos_table, const float* sin_table,
                        float* query_out, float* key_out, const RopeShape& shape, hipStream_t stream) {

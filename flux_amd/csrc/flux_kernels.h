@@ -93,8 +93,6 @@ hipError_t launch_install_state(const int64_t* token_src, int64_t position_value
                                 bool write_generated0, int64_t* input_token, int64_t* position, int64_t* cache_length,
                                 int64_t* step, int64_t* generated, int32_t* error, int32_t* host_error,
                                 hipStream_t stream);
-// *position += 1 (one thread; the layer runtime's step epilogue).
-hipError_t launch_advance_position(int64_t* position, hipStream_t stream);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, float* out, int64_t rows, int cols, float eps,
                                hipStream_t stream);
 hipError_t launch_residual_rmsnorm_rows(const float* hidden, const float* residual, const float* w, float* norm_out,
