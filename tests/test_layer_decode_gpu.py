@@ -129,3 +129,37 @@ def test_layer_capacity_and_validation(layer_setup, gpu_device):
     assert runtime.workspace_bytes() > 0 and runtime.workspace().numel() * 4 == runtime.workspace_bytes()
     # Every replay above was one launch of the fused kernel's single-layer step on one stream.
     assert runtime.replay_launches() == (2, 2)
+
+
+def test_layer_step_reads_hidden_in_stream_order(layer_setup, gpu_device):
+    """A step reads the caller's hidden state itself (no copy): its output feeds the next
+    step directly (the output buffer is read and rewritten by the same step), and a caller
+    buffer rewritten on the same stream after replay() does not change the step that
+    reads it.  Every output equals the oracle's chained decoder-layer steps."""
+    oracle, _ = layer_setup
+    g = torch.Generator().manual_seed(5)
+    position = 21
+    keys = torch.randn(1, 3, position, 64, generator=g)
+    values = torch.randn(1, 3, position, 64, generator=g)
+    first = torch.randn(1, 1, 576, generator=g)
+    runtime = _runtime(layer_setup, gpu_device, 64, position, first.to(gpu_device), keys.to(gpu_device),
+                       values.to(gpu_device))
+    cache = OracleCache()
+    cache.keys = [None] * LAYER + [keys]
+    cache.values = [None] * LAYER + [values]
+    hidden = first
+    scratch = first.to(gpu_device).clone()
+    for step in range(6):
+        if step % 2 == 0:
+            out = runtime.replay(scratch)
+            scratch.fill_(float("nan"))  # stream-ordered after the step that reads it
+        else:
+            out = runtime.replay(runtime.output())
+        expected = _oracle_step(oracle, cache, hidden, position + step)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu(), expected, rtol=1e-4, atol=1e-4)
+        hidden = expected
+        if step % 2 == 1:
+            scratch.copy_(out)
+    assert runtime.position() == position + 6
+    assert runtime.replay_launches() == (6, 6)
