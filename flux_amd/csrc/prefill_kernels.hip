@@ -701,6 +701,169 @@ __global__ void __launch_bounds__(64 * kSplitWaves) gemm_split_kernel(GemmArgs a
     }
 }
 
+// Small-M GEMM on v_mfma_f32_16x16x4f32 with the operands loaded straight into registers.
+// Block = kRegWaves waves (three per SIMD), output tile (16 RT) rows x kCols columns; wave w
+// sums the w-th of kRegWaves contiguous K slices (48 values at K = 576).  Lane l loads float4s
+// of four consecutive K values from memory (L2): A rows l % 16 (+ 16 rt), B columns l % 16
+// (+ 16 jb), K values 4 (l / 16) .. + 3 of each 16-value stage, so k-step s of the stage pairs
+// component s of every operand (the MFMA's K index l / 16 stands for K value 4 (l / 16) + s).
+// A ring of kDepth stages is in flight; at K = 576 it holds the whole slice, so each wave
+// issues all of its loads at once and pays one memory round trip.  The LDS ring of
+// gemm_split_kernel is shallower than a round trip at one wave per SIMD, and its K split
+// needs a reduce kernel.  The waves' partial tiles are summed in LDS in K order and the block
+// shares the epilogue.
+constexpr int kRegWaves = 12;
+
+// Scheduling barriers keep every load where it is issued: left free, the compiler sinks the
+// loads to their uses (fewer live registers) and the ring is gone.
+template <int kStages, int kDepth, typename Issue, typename Compute>
+__device__ __forceinline__ void reg_pipeline(Issue&& issue, Compute&& compute) {
+    static_for<0, (kStages < kDepth ? kStages : kDepth)>([&](auto st) { issue(st); });
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, kStages>([&](auto st) {
+        compute(st);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(st)::value + kDepth < kStages) {
+            issue(std::integral_constant<int, decltype(st)::value + kDepth>{});
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    });
+}
+
+template <GemmEpilogue E, int RT, int kCols, bool kNorm, int kK>
+__global__ void __launch_bounds__(64 * kRegWaves) gemm_reg_kernel(GemmArgs args) {
+    static_assert(kK % (kRegWaves * 16) == 0, "whole 16-value stages per wave");
+    static_assert(kCols == 32 || kCols == 64, "16-column blocks of a 32- or 64-column tile");
+    static_assert(kCols == 64 || (E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual),
+                  "column pairs (RoPE, SwiGLU) need 64-column tiles");
+    static_assert(!kNorm || kK == kHidden, "the folded norm spans the hidden width");
+    constexpr int kJB = kCols / 16;
+    constexpr int kRows = 16 * RT;
+    constexpr int kStages = kK / (kRegWaves * 16);
+    constexpr int kPerStage = RT + kJB + (kNorm ? 1 : 0);  // float4 loads per lane per stage
+    // Ring stages: as many as 72 registers hold (three waves share a SIMD's 512 per lane).
+    constexpr int kRingRegs = 72;
+    constexpr int kDepthFit = kRingRegs / (4 * kPerStage) < 2 ? 2 : kRingRegs / (4 * kPerStage);
+    constexpr int kDepth = kDepthFit < 9 ? kDepthFit : 9;
+    __shared__ float partial[kRegWaves][kRows][kCols + 1];
+    __shared__ float norm_ss[kNorm ? kRegWaves : 1][kRows];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kRows;
+    const int n0 = static_cast<int>(blockIdx.x) * kCols;
+    const int kq = lane >> 4;
+    const int r16 = lane & 15;
+    const int k_first = wave * (kK / kRegWaves) + 4 * kq;  // this lane's first K value
+
+    const float* a_src[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int64_t row = m0 + 16 * rt + r16 < args.m ? m0 + 16 * rt + r16 : args.m - 1;
+        a_src[rt] = args.a + row * kK + k_first;
+    }
+    const float* b_src[kJB];
+#pragma unroll
+    for (int jb = 0; jb < kJB; ++jb)
+        b_src[jb] = args.b + static_cast<int64_t>(b_row<E>(n0 + 16 * jb + r16, args.n)) * kK + k_first;
+    const float* g_src = kNorm ? args.norm_weight + k_first : nullptr;
+
+    f32x4 ring_a[kDepth][RT];
+    f32x4 ring_b[kDepth][kJB];
+    f32x4 ring_g[kNorm ? kDepth : 1];
+    auto issue = [&](auto st) {
+        constexpr int s = decltype(st)::value;
+        constexpr int slot = s % kDepth;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) ring_a[slot][rt] = *reinterpret_cast<const f32x4*>(a_src[rt] + 16 * s);
+#pragma unroll
+        for (int jb = 0; jb < kJB; ++jb) ring_b[slot][jb] = *reinterpret_cast<const f32x4*>(b_src[jb] + 16 * s);
+        if constexpr (kNorm) ring_g[slot] = *reinterpret_cast<const f32x4*>(g_src + 16 * s);
+    };
+    f32x4 acc[RT][kJB];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int jb = 0; jb < kJB; ++jb) acc[rt][jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ss[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) ss[rt] = 0.0f;
+    auto compute = [&](auto st) {
+        constexpr int slot = decltype(st)::value % kDepth;
+        f32x4 a[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            a[rt] = ring_a[slot][rt];
+            if constexpr (kNorm) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ss[rt] = fmaf(a[rt][e], a[rt][e], ss[rt]);
+                    a[rt][e] *= ring_g[slot][e];
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int jb = 0; jb < kJB; ++jb)
+                    acc[rt][jb] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(a[rt][s], ring_b[slot][jb][s], acc[rt][jb], 0, 0, 0);
+    };
+    reg_pipeline<kStages, kDepth>(issue, compute);
+
+    // D[row 4 (l / 16) + r][column l % 16] of each 16 x 16 block.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int jb = 0; jb < kJB; ++jb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) partial[wave][16 * rt + 4 * kq + r][16 * jb + r16] = acc[rt][jb][r];
+    if constexpr (kNorm) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float v = ss[rt];
+            v += __shfl_xor(v, 16, kWave);
+            v += __shfl_xor(v, 32, kWave);
+            if (lane < 16) norm_ss[wave][16 * rt + lane] = v;
+        }
+    }
+    __syncthreads();
+    auto total = [&](int row, int col) {
+        float t = partial[0][row][col];
+#pragma unroll
+        for (int w = 1; w < kRegWaves; ++w) t += partial[w][row][col];
+        return t;
+    };
+    auto inv_rms = [&](int row) {
+        if constexpr (kNorm) {
+            float t = norm_ss[0][row];
+#pragma unroll
+            for (int w = 1; w < kRegWaves; ++w) t += norm_ss[w][row];
+            return rms_inverse(t, kHidden, args.norm_eps);
+        } else {
+            return 1.0f;
+        }
+    };
+    if constexpr (E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual) {
+        for (int i = static_cast<int>(threadIdx.x); i < kRows * kCols; i += 64 * kRegWaves) {
+            const int row = i / kCols, col = i % kCols;
+            const int64_t out_row = m0 + row;
+            if (out_row < args.m) gemm_store_one<E>(args, out_row, n0 + col, total(row, col) * inv_rms(row));
+        }
+    } else {
+        // Column pairs j / j + 32 of the 64-column group (the RoPE pair, or gate and up).
+        for (int i = static_cast<int>(threadIdx.x); i < kRows * 32; i += 64 * kRegWaves) {
+            const int row = i / 32, j = i % 32;
+            const int64_t out_row = m0 + row;
+            if (out_row >= args.m) continue;
+            const float inv = inv_rms(row);
+            gemm_store_pair<E>(args, out_row, n0, j, total(row, j) * inv, total(row, j + 32) * inv);
+        }
+    }
+}
+
 // Sums the kPlanes partial planes of a K-split gemm_split_kernel or gemm_narrow_kernel in plane order and
 // applies the epilogue: thread -> (row, column pair j / j + 32 of a 64-column group) for
 // kCols = 64, (row, column) for kCols = 32.  The folded norm's row scale comes from the
@@ -1531,10 +1694,68 @@ static SplitShape split_shape(const GemmArgs& args, GemmEpilogue epilogue) {
     return {0, 0};
 }
 
-// gemm_split_kernel folds an RMSNorm of the A rows into the QKV and gate/up GEMMs (K = hidden).
+// Tiling of gemm_reg_kernel (rt = 0 when it does not take the GEMM): 16-row blocks with the
+// narrowest column tile whose grid fits the device once (one block per CU), for the GEMMs over
+// the hidden width (QKV, o_proj, gate/up).  The down projection (K = intermediate) measured
+// faster on gemm_split_kernel at every prompt length.
+#ifndef FLUX_REG_GEMM
+#define FLUX_REG_GEMM 1
+#endif
+struct RegShape {
+    int rt;
+    int cols;
+};
+static RegShape reg_shape(const GemmArgs& args, GemmEpilogue epilogue) {
+    if (!FLUX_REG_GEMM || args.k != kHidden || args.n % 64 != 0) return {0, 0};
+    const bool pair = epilogue == GemmEpilogue::kQkvRope || epilogue == GemmEpilogue::kSwiglu;
+    const int64_t r16 = (args.m + 15) / 16;
+    if (!pair && (args.n / 32) * r16 <= kSplitBlocks) return {1, 32};
+    if ((args.n / 64) * r16 <= kSplitBlocks) return {1, 64};
+    return {0, 0};
+}
+
+// gemm_reg_kernel and gemm_split_kernel fold an RMSNorm of the A rows into the QKV and gate/up
+// GEMMs (K = hidden).
 static bool split_folds_norm(const GemmArgs& args, GemmEpilogue epilogue) {
     return args.k == kHidden && (epilogue == GemmEpilogue::kQkvRope || epilogue == GemmEpilogue::kSwiglu) &&
-           split_shape(args, epilogue).rt != 0;
+           (reg_shape(args, epilogue).rt != 0 || split_shape(args, epilogue).rt != 0);
+}
+
+static hipError_t launch_reg(const GemmArgs& args, GemmEpilogue epilogue, RegShape shape, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(args.n / shape.cols), static_cast<unsigned>((args.m + 16 * shape.rt - 1) /
+                                                                                   (16 * shape.rt)));
+    const dim3 block(64 * kRegWaves);
+    const bool norm = args.norm_weight != nullptr;
+#define FLUX_REG(E, COLS, NORM) \
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_reg_kernel<E, 1, COLS, NORM, kHidden>), grid, block, 0, stream, args)
+#define FLUX_REG_PLAIN(E)                       \
+    do {                                        \
+        if (shape.cols == 32) FLUX_REG(E, 32, false); \
+        else FLUX_REG(E, 64, false);            \
+    } while (0)
+#define FLUX_REG_PAIR(E)                        \
+    do {                                        \
+        if (norm) FLUX_REG(E, 64, true);        \
+        else FLUX_REG(E, 64, false);            \
+    } while (0)
+    switch (epilogue) {
+        case GemmEpilogue::kStore:
+            FLUX_REG_PLAIN(GemmEpilogue::kStore);
+            break;
+        case GemmEpilogue::kResidual:
+            FLUX_REG_PLAIN(GemmEpilogue::kResidual);
+            break;
+        case GemmEpilogue::kSwiglu:
+            FLUX_REG_PAIR(GemmEpilogue::kSwiglu);
+            break;
+        case GemmEpilogue::kQkvRope:
+            FLUX_REG_PAIR(GemmEpilogue::kQkvRope);
+            break;
+    }
+#undef FLUX_REG_PAIR
+#undef FLUX_REG_PLAIN
+#undef FLUX_REG
+    return hipGetLastError();
 }
 
 // K parts of the 576-column kernel: kSplitBlocksK while that grid is at most
@@ -1588,10 +1809,12 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
-    const SplitShape shape = split_shape(args, epilogue);
-    const int rt = shape.rt;
     const bool norm = args.norm_weight != nullptr;
     if (norm && !split_folds_norm(args, epilogue)) return hipErrorInvalidValue;
+    const RegShape reg = reg_shape(args, epilogue);
+    if (reg.rt != 0) return launch_reg(args, epilogue, reg, stream);
+    const SplitShape shape = split_shape(args, epilogue);
+    const int rt = shape.rt;
     if (rt != 0) {
         const bool hidden = args.k == kHidden;
         dim3 grid(static_cast<unsigned>(args.n / shape.cols), static_cast<unsigned>((args.m + 32 * rt - 1) / (32 * rt)));

@@ -242,16 +242,18 @@ def test_lm_head_argmax(gpu_device, vocab):
     assert int(token.item()) == ref.greedy_argmax(logits.cpu().numpy())
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 64, 16), (70, 576, 48), (64, 192, 32), (130, 960, 576), (257, 576, 1536),
-                                   (512, 576, 1536), (600, 1024, 576), (1200, 1024, 576), (1000, 576, 1536),
-                                   (2048, 576, 1536), (300, 1024, 64), (300, 576, 64), (1024, 3072, 576)])
+@pytest.mark.parametrize("m,n,k", [(1, 64, 16), (70, 576, 48), (64, 192, 32), (16, 576, 576), (200, 576, 576),
+                                   (130, 960, 576), (257, 576, 1536), (512, 576, 1536), (600, 1024, 576),
+                                   (1200, 1024, 576), (1000, 576, 1536), (2048, 576, 1536), (300, 1024, 64),
+                                   (300, 576, 64), (1024, 3072, 576)])
 def test_mfma_linear(gpu_device, m, n, k):
-    # k = 576 or 1536 with at most 256 tiles: the split kernel, on 32 x 32 tiles (130, 257 rows),
-    # else on (32 RT) x 64 tiles with RT = 1 (512 rows), 2 (600 rows) or 4 (1200 rows); widths
-    # that are not a multiple of 128 only with RT = 1. Otherwise those widths take the 64 x 64
-    # tile kernel when k % 32 == 0 (1000, 2048 rows), else the 128-column kernel; grids under 256
-    # blocks take their four-buffer ring variants (300 rows with k = 64, 1000 rows, and the
-    # first three cases).
+    # k = 576 with at most 256 16-row tiles: the register kernel, 32 columns wide (16, 200 rows)
+    # or 64 (130 rows).  Otherwise k = 576 or 1536 with at most 256 tiles: the split kernel, on
+    # 32 x 32 tiles (257 rows), else on (32 RT) x 64 tiles with RT = 1 (512 rows), 2 (600 rows)
+    # or 4 (1200 rows); widths that are not a multiple of 128 only with RT = 1. Otherwise those
+    # widths take the 64 x 64 tile kernel when k % 32 == 0 (1000, 2048 rows), else the
+    # 128-column kernel; grids under 256 blocks take their four-buffer ring variants (300 rows
+    # with k = 64, 1000 rows, and the first three cases).
     a = _randn(m, k, seed=61).to(gpu_device)
     w = _randn(n, k, seed=62, std=0.05).to(gpu_device)
     r = _randn(m, n, seed=63).to(gpu_device)
@@ -268,7 +270,8 @@ def test_mfma_linear(gpu_device, m, n, k):
 
 @pytest.mark.parametrize("rows", [1, 77, 300, 600])
 def test_gate_up_swiglu_rows(gpu_device, rows):
-    # 1 / 77: split kernel with one 32-row tile per block, 300: two, 600: four.
+    # 1 / 77: register kernel (16-row tiles), 300: split kernel with two 32-row tiles per block,
+    # 600: four.
     x = _randn(rows, H, seed=71).to(gpu_device)
     gu = _randn(2 * I, H, seed=72, std=0.02).to(gpu_device)
     out = torch.empty(rows, I, device=gpu_device)
@@ -282,7 +285,8 @@ def test_gate_up_swiglu_rows(gpu_device, rows):
 
 @pytest.mark.parametrize("rows,capacity", [(1, 8), (129, 200), (512, 8704), (1900, 2048)])
 def test_qkv_rope_cache_rows(gpu_device, rows, capacity):
-    # 1 to 512 rows: split kernel with one 32-row tile per block; 1900: four per block.
+    # 1 / 129 rows: register kernel (16-row tiles); 512: split kernel with one 32-row tile per
+    # block; 1900: four per block.
     x = _randn(rows, H, seed=81).to(gpu_device)
     qkv = _randn(960, H, seed=82, std=0.02).to(gpu_device)
     cos, sin = rope_table(OracleConfig(), capacity)
