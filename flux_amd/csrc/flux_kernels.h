@@ -134,6 +134,14 @@ struct GemmArgs {
     // epilogue.  Null: every block covers all of K.
     float* split_partials;
     int64_t split_floats;  // floats available at split_partials: no split whose planes exceed it
+    // Optional A given unreduced (QKV with the folded norm on gemm_reg_kernel only, see
+    // gemm_sums_planes): A = a_residual + (plane 0 + plane 1 + plane 2) of the kSplitBlocksK
+    // planes [M, K] at a_planes that launch_gemm_planes left, summed in the order of the reduce
+    // kernel, so A is bitwise the rows that reduce would have written.  The blocks of the first
+    // column tile also write those rows to a_rows_out.  args.a is then not read.
+    const float* a_planes;
+    const float* a_residual;
+    float* a_rows_out;
 };
 
 // Blocks that share one output tile's K range when GemmArgs::split_partials is given.
@@ -155,6 +163,16 @@ hipError_t launch_norm_gemm(const GemmArgs& args, const float* norm_weight, floa
                             GemmEpilogue epilogue, hipStream_t stream);
 // True when launch_norm_gemm folds the RMSNorm into this GEMM (no separate norm launch).
 bool gemm_folds_norm(const GemmArgs& args, GemmEpilogue epilogue);
+// True when launch_gemm splits K over kSplitBlocksK blocks for these args (partial planes in
+// args.split_partials, then a reduce kernel).
+bool gemm_writes_planes(const GemmArgs& args, GemmEpilogue epilogue);
+// The split kernel alone for args where gemm_writes_planes holds: the kSplitBlocksK partial
+// planes are left in args.split_partials unreduced (args.c and args.residual are not touched)
+// for a GEMM that sums them into its A rows.
+hipError_t launch_gemm_planes(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream);
+// True when launch_gemm takes GemmArgs::a_planes for this GEMM (shape and epilogue; the folded
+// norm must be given too).
+bool gemm_sums_planes(const GemmArgs& args, GemmEpilogue epilogue);
 // c = residual + A·Wᵀ (args with the residual epilogue) and norm_out = rmsnorm(c) with the
 // given weights: the norm that the next GEMM needs when it does not fold it.  A K-split
 // 576-column GEMM reduces its partial planes inside the norm kernel.

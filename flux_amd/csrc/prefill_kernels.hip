@@ -730,19 +730,22 @@ __device__ __forceinline__ void reg_pipeline(Issue&& issue, Compute&& compute) {
     });
 }
 
-template <GemmEpilogue E, int RT, int kCols, bool kNorm, int kK>
+template <GemmEpilogue E, int RT, int kCols, bool kNorm, int kK, bool kSumA = false>
 __global__ void __launch_bounds__(64 * kRegWaves) gemm_reg_kernel(GemmArgs args) {
     static_assert(kK % (kRegWaves * 16) == 0, "whole 16-value stages per wave");
     static_assert(kCols == 32 || kCols == 64, "16-column blocks of a 32- or 64-column tile");
     static_assert(kCols == 64 || (E == GemmEpilogue::kStore || E == GemmEpilogue::kResidual),
                   "column pairs (RoPE, SwiGLU) need 64-column tiles");
     static_assert(!kNorm || kK == kHidden, "the folded norm spans the hidden width");
+    static_assert(!kSumA || kSplitBlocksK == 3, "A summed from three planes");
+    constexpr int kAParts = kSumA ? 4 : 1;  // residual + three planes, or the A rows
     constexpr int kJB = kCols / 16;
     constexpr int kRows = 16 * RT;
     constexpr int kStages = kK / (kRegWaves * 16);
-    constexpr int kPerStage = RT + kJB + (kNorm ? 1 : 0);  // float4 loads per lane per stage
-    // Ring stages: as many as 72 registers hold (three waves share a SIMD's 512 per lane).
-    constexpr int kRingRegs = 72;
+    constexpr int kPerStage = RT * kAParts + kJB + (kNorm ? 1 : 0);  // float4 loads per lane per stage
+    // Ring stages: as many as 72 registers hold (three waves share a SIMD's 512 per lane), 108
+    // when A comes as four parts, so the whole slice is still in flight at once.
+    constexpr int kRingRegs = kSumA ? 108 : 72;
     constexpr int kDepthFit = kRingRegs / (4 * kPerStage) < 2 ? 2 : kRingRegs / (4 * kPerStage);
     constexpr int kDepth = kDepthFit < 9 ? kDepthFit : 9;
     __shared__ float partial[kRegWaves][kRows][kCols + 1];
@@ -756,11 +759,20 @@ __global__ void __launch_bounds__(64 * kRegWaves) gemm_reg_kernel(GemmArgs args)
     const int r16 = lane & 15;
     const int k_first = wave * (kK / kRegWaves) + 4 * kq;  // this lane's first K value
 
-    const float* a_src[RT];
+    // Part 0 is the A rows (or the residual when A is summed); parts 1-3 the planes.
+    const float* a_src[RT][kAParts];
+    int64_t a_row[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const int64_t row = m0 + 16 * rt + r16 < args.m ? m0 + 16 * rt + r16 : args.m - 1;
-        a_src[rt] = args.a + row * kK + k_first;
+        a_row[rt] = m0 + 16 * rt + r16;
+        const int64_t row = a_row[rt] < args.m ? a_row[rt] : args.m - 1;
+        if constexpr (kSumA) {
+            a_src[rt][0] = args.a_residual + row * kK + k_first;
+#pragma unroll
+            for (int b = 0; b < 3; ++b) a_src[rt][1 + b] = args.a_planes + (b * args.m + row) * kK + k_first;
+        } else {
+            a_src[rt][0] = args.a + row * kK + k_first;
+        }
     }
     const float* b_src[kJB];
 #pragma unroll
@@ -768,14 +780,17 @@ __global__ void __launch_bounds__(64 * kRegWaves) gemm_reg_kernel(GemmArgs args)
         b_src[jb] = args.b + static_cast<int64_t>(b_row<E>(n0 + 16 * jb + r16, args.n)) * kK + k_first;
     const float* g_src = kNorm ? args.norm_weight + k_first : nullptr;
 
-    f32x4 ring_a[kDepth][RT];
+    f32x4 ring_a[kDepth][RT][kAParts];
     f32x4 ring_b[kDepth][kJB];
     f32x4 ring_g[kNorm ? kDepth : 1];
     auto issue = [&](auto st) {
         constexpr int s = decltype(st)::value;
         constexpr int slot = s % kDepth;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) ring_a[slot][rt] = *reinterpret_cast<const f32x4*>(a_src[rt] + 16 * s);
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int part = 0; part < kAParts; ++part)
+                ring_a[slot][rt][part] = *reinterpret_cast<const f32x4*>(a_src[rt][part] + 16 * s);
 #pragma unroll
         for (int jb = 0; jb < kJB; ++jb) ring_b[slot][jb] = *reinterpret_cast<const f32x4*>(b_src[jb] + 16 * s);
         if constexpr (kNorm) ring_g[slot] = *reinterpret_cast<const f32x4*>(g_src + 16 * s);
@@ -793,7 +808,16 @@ __global__ void __launch_bounds__(64 * kRegWaves) gemm_reg_kernel(GemmArgs args)
         f32x4 a[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            a[rt] = ring_a[slot][rt];
+            if constexpr (kSumA) {
+                const f32x4* part = ring_a[slot][rt];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[rt][e] = part[0][e] + ((part[1][e] + part[2][e]) + part[3][e]);
+                if (blockIdx.x == 0 && a_row[rt] < args.m)
+                    *reinterpret_cast<f32x4*>(args.a_rows_out + a_row[rt] * kK + k_first + 16 * decltype(st)::value) =
+                        a[rt];
+            } else {
+                a[rt] = ring_a[slot][rt][0];
+            }
             if constexpr (kNorm) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -1738,6 +1762,11 @@ static hipError_t launch_reg(const GemmArgs& args, GemmEpilogue epilogue, RegSha
         if (norm) FLUX_REG(E, 64, true);        \
         else FLUX_REG(E, 64, false);            \
     } while (0)
+    if (args.a_planes != nullptr) {
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_reg_kernel<GemmEpilogue::kQkvRope, 1, 64, true, kHidden, true>), grid,
+                           block, 0, stream, args);
+        return hipGetLastError();
+    }
     switch (epilogue) {
         case GemmEpilogue::kStore:
             FLUX_REG_PLAIN(GemmEpilogue::kStore);
@@ -1805,14 +1834,59 @@ static bool narrow_shape(const GemmArgs& args, GemmEpilogue epilogue) {
            args.k % 32 == 0;
 }
 
-hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Whether gemm_split_kernel takes these args with K split over kSplitBlocksK blocks: its grid
+// fits the device once even when tripled, and the caller's planes hold the split.
+static bool split_k_taken(const GemmArgs& args, GemmEpilogue epilogue) {
+    const SplitShape shape = split_shape(args, epilogue);
+    if (shape.rt == 0) return false;
+    const int64_t blocks = (args.n / shape.cols) * ((args.m + 32 * shape.rt - 1) / (32 * shape.rt));
+    return planes_fit(args, kSplitBlocksK) && blocks * kSplitBlocksK <= kSplitKBlocks;
+}
+
+bool gemm_writes_planes(const GemmArgs& args, GemmEpilogue epilogue) {
+    return reg_shape(args, epilogue).rt == 0 && split_k_taken(args, epilogue);
+}
+
+bool gemm_sums_planes(const GemmArgs& args, GemmEpilogue epilogue) {
+    return epilogue == GemmEpilogue::kQkvRope && reg_shape(args, epilogue).rt != 0;
+}
+
+static hipError_t gemm_args_valid(const GemmArgs& args, GemmEpilogue epilogue) {
     if (args.k % kBK != 0 || args.n % 64 != 0 || args.m <= 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kSwiglu && args.n % kBN != 0) return hipErrorInvalidValue;
     if (epilogue == GemmEpilogue::kQkvRope && args.n != kQKV) return hipErrorInvalidValue;
     const bool norm = args.norm_weight != nullptr;
     if (norm && !split_folds_norm(args, epilogue)) return hipErrorInvalidValue;
+    if (args.a_planes != nullptr && (!gemm_sums_planes(args, epilogue) || !norm || args.a_residual == nullptr ||
+                                     args.a_rows_out == nullptr || !aligned16(args.a_planes) ||
+                                     !aligned16(args.a_residual) || !aligned16(args.a_rows_out)))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+static hipError_t launch_gemm_split(const GemmArgs& args, GemmEpilogue epilogue, bool reduce, hipStream_t stream);
+
+hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
+    const hipError_t valid = gemm_args_valid(args, epilogue);
+    if (valid != hipSuccess) return valid;
     const RegShape reg = reg_shape(args, epilogue);
     if (reg.rt != 0) return launch_reg(args, epilogue, reg, stream);
+    return launch_gemm_split(args, epilogue, true, stream);
+}
+
+hipError_t launch_gemm_planes(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t stream) {
+    const hipError_t valid = gemm_args_valid(args, epilogue);
+    if (valid != hipSuccess) return valid;
+    if (args.a_planes != nullptr || !gemm_writes_planes(args, epilogue)) return hipErrorInvalidValue;
+    return launch_gemm_split(args, epilogue, false, stream);
+}
+
+// gemm_split_kernel and the remaining kernels of launch_gemm; `reduce` false stops after the
+// partial planes of a K split.
+static hipError_t launch_gemm_split(const GemmArgs& args, GemmEpilogue epilogue, bool reduce, hipStream_t stream) {
+    const bool norm = args.norm_weight != nullptr;
     const SplitShape shape = split_shape(args, epilogue);
     const int rt = shape.rt;
     if (rt != 0) {
@@ -1821,8 +1895,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
         const dim3 split_block(64 * kSplitWaves);
         // Grids of at most a third of the device split K over kSplitBlocksK blocks when the
         // caller provides the partial planes.
-        const bool split_k = planes_fit(args, kSplitBlocksK) &&
-                             static_cast<int64_t>(grid.x) * grid.y * kSplitBlocksK <= kSplitKBlocks;
+        const bool split_k = split_k_taken(args, epilogue);
         if (split_k) grid.x *= kSplitBlocksK;
 #define FLUX_SPLIT_RT(E, ST, RT, NORM, COLS)                                                                        \
     do {                                                                                                            \
@@ -1879,7 +1952,7 @@ hipError_t launch_gemm(const GemmArgs& args, GemmEpilogue epilogue, hipStream_t 
 #undef FLUX_LAUNCH_SPLIT
 #undef FLUX_SPLIT_RT
         hipError_t st = hipGetLastError();
-        if (st != hipSuccess || !split_k) return st;
+        if (st != hipSuccess || !split_k || !reduce) return st;
         const int64_t units = shape.cols == 64 ? args.n / 2 : args.n;
         const dim3 rgrid(static_cast<unsigned>((args.m * units + 255) / 256));
 #define FLUX_REDUCE(E, NORM, COLS) \
@@ -1982,11 +2055,10 @@ hipError_t launch_gemm_residual_norm(const GemmArgs& args, const float* norm_wei
                                      hipStream_t stream) {
     // The fused kernel reads and writes rows as float4: every buffer must be 16-byte aligned
     // (a norm weight that is a view into a larger tensor may not be), else the plain path runs.
-    auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     const bool fusable = narrow_shape(args, GemmEpilogue::kResidual) && args.n == kHidden &&
-                         split_shape(args, GemmEpilogue::kResidual).rt == 0 && aligned(args.c) &&
-                         aligned(args.residual) && aligned(args.split_partials) && aligned(norm_weight) &&
-                         aligned(norm_out);
+                         split_shape(args, GemmEpilogue::kResidual).rt == 0 && aligned16(args.c) &&
+                         aligned16(args.residual) && aligned16(args.split_partials) && aligned16(norm_weight) &&
+                         aligned16(norm_out);
     const int parts = fusable ? narrow_parts(args, true) : 1;
     if (parts == 1) {
         const hipError_t e = launch_gemm(args, GemmEpilogue::kResidual, stream);

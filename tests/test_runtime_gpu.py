@@ -457,13 +457,15 @@ def test_prefill_input_errors(small_model):
         native.prefill(ids[:, :-1])
 
 
-@pytest.mark.parametrize("length", [1, 45, 333, 512, 513, 1024, 1025, 1537, 3001])
+@pytest.mark.parametrize("length", [1, 7, 9, 45, 333, 512, 513, 1024, 1025, 1537, 3001])
 def test_odd_length_prefill_matches_oracle(small_model, length):
     """Prompt lengths that end inside a 128-query attention tile and split the keys of the
     later tiles into chunks (333: 2-tile, 1537: 4-tile, 3001: 8-tile chunks), through the whole
     native prefill, against the CPU oracle: last-row logits, greedy token, K/V cache rows.
-    Short prompts also take the split GEMMs that fold the RMSNorm (1 and 45 rows end inside
-    the first 32-row tile).  512 | 513 straddle the one-kernel
+    Short prompts also take the GEMMs that fold the RMSNorm (1, 7, 9 and 45 rows end inside
+    the first 16-row tile of the register kernel or 32-row tile of the split kernel).  1 | 7 | 9:
+    up to 8 rows the next layer's QKV kernel sums the down GEMM's partial planes and residual
+    (no reduce kernel), 9 rows take the reduce.  512 | 513 straddle the one-kernel
     attention's limit (512 tokens), and 1024 | 1025 the limit up to which the K-split planes
     are sized for gate/up (1024 rows), so both sides of each switch run."""
     g = torch.Generator().manual_seed(length)
