@@ -1155,7 +1155,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_narrow_kernel(GemmArgs args
 constexpr int kQTile = 128;
 constexpr int kKTile = 64;
 constexpr int kAttnThreads = 256;
-constexpr int kMaxChunkTiles = 16;  // 1024 keys: 24 (1536) measured 1.5% slower at 8192 tokens
+constexpr int kMaxChunkTiles = 16;  // 1024 keys: 24 (1536) measured 1.5% slower at 8192 tokens, 12 / 14 0.1%
 constexpr int kPartialRow = kHeadDim + 4;  // o[64], m, l, 2 words of padding (16-byte rows)
 constexpr int kMergeMaxChunks = 16;        // >= the chunks of any query tile up to kMaxCapacity
 constexpr int kKVTileFloats = kKTile * kHeadDim;
