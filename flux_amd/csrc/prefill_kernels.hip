@@ -149,14 +149,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& args, const f32x16
     }
 }
 
-// C = epilogue(A[M,K] * W[N,K]^T) on v_mfma_f32_32x32x2f32.  Block tile (64*MI) x 128,
-// 4 waves in 2 x 2, wave tile (32*MI) x 64.  K is consumed 16 at a time; MFMA
-// instruction s (0..7) of a stage pairs K index s (lanes 0-31) with s + 8 (lanes
-// 32-63), so each lane reads its 8 K values of a row with two ds_read_b128.
+// C = epilogue(A[M,K] * W[N,K]^T) on v_mfma_f32_32x32x2f32.  Block tile (32*MI*kWaves/2) x 128,
+// kWaves waves in kWaves/2 x 2, wave tile (32*MI) x 64.  The 128-row tile of QKV runs as 8 waves
+// of 32 x 64 (MI = 1) rather than 4 of 64 x 64: its 512 blocks fill the device in one round at
+// two per CU, and four waves per SIMD hide the operand reads and epilogue better than two
+// (8192 tokens: 34.89 -> 34.75 ms; gate/up, three rounds deep, was slower that way).
+// K is consumed 16 at a time; MFMA instruction s (0..7) of a stage pairs K index s (lanes
+// 0-31) with s + 8 (lanes 32-63), so each lane reads its 8 K values of a row with two
+// ds_read_b128.
 // Tiles stream HBM -> LDS with global_load_lds (no register staging), double buffered.
-template <GemmEpilogue E, int MI>
-__global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
-    constexpr int kBMt = 64 * MI;
+template <GemmEpilogue E, int MI, int kWaves = 4>
+__global__ void __launch_bounds__(64 * kWaves) gemm_kernel(GemmArgs args) {
+    static_assert(kWaves == 4 || kWaves == 8, "waves in kWaves / 2 rows x 2 column groups");
+    constexpr int kBMt = 32 * MI * (kWaves / 2);
     __shared__ __align__(16) float a_s[2][kBMt * kBK];
     __shared__ __align__(16) float b_s[2][kBN * kBK];
 
@@ -169,30 +174,30 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_kernel(GemmArgs args) {
     const int K = args.k;
     const bool group_valid = n0 + wn * 64 < args.n;
 
-    // Rows this wave streams: A blocks i = wave + 4j (16 rows each), B blocks likewise.
-    constexpr int kABlocks = kBMt / 16;            // 4 or 8
-    constexpr int kAPerWave = kABlocks / 4;        // 1 or 2
+    // Rows this wave streams: A blocks i = wave + kWaves j (16 rows each), B blocks likewise.
+    constexpr int kAPerWave = kBMt / 16 / kWaves;  // 1 or 2
+    constexpr int kBPerWave = kBN / 16 / kWaves;   // 2 or 1
     const float* a_src[kAPerWave];
-    const float* b_src[2];
+    const float* b_src[kBPerWave];
 #pragma unroll
     for (int j = 0; j < kAPerWave; ++j) {
-        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+        const int row = 16 * (wave + kWaves * j) + (lane >> 2);
         const int64_t gr = m0 + row < args.m ? m0 + row : args.m - 1;
         a_src[j] = args.a + gr * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int row = 16 * (wave + 4 * j) + (lane >> 2);
+    for (int j = 0; j < kBPerWave; ++j) {
+        const int row = 16 * (wave + kWaves * j) + (lane >> 2);
         const int col = n0 + row < args.n ? n0 + row : args.n - 1;
         b_src[j] = args.b + static_cast<int64_t>(b_row<E>(col, args.n)) * K + 4 * ((lane & 3) ^ ((row >> 2) & 3));
     }
     auto issue_stage = [&](int k0, int buf) {
 #pragma unroll
         for (int j = 0; j < kAPerWave; ++j)
-            lds_copy16(a_src[j] + k0, &a_s[buf][(wave + 4 * j) * 16 * kBK]);
+            lds_copy16(a_src[j] + k0, &a_s[buf][(wave + kWaves * j) * 16 * kBK]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            lds_copy16(b_src[j] + k0, &b_s[buf][(wave + 4 * j) * 16 * kBK]);
+        for (int j = 0; j < kBPerWave; ++j)
+            lds_copy16(b_src[j] + k0, &b_s[buf][(wave + kWaves * j) * 16 * kBK]);
     };
 
     f32x16 acc[MI][2];
@@ -2018,7 +2023,9 @@ static hipError_t launch_gemm_split(const GemmArgs& args, GemmEpilogue epilogue,
     const bool small = static_cast<int64_t>(grid.x) * grid.y < kRingBlocks;
 #define FLUX_LAUNCH_GEMM(E)                                                                    \
     do {                                                                                       \
-        if (big)                                                                               \
+        if (big && E == GemmEpilogue::kQkvRope)                                                \
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 1, 8>), grid, dim3(512), 0, stream, args);      \
+        else if (big)                                                                          \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_kernel<E, 2>), grid, block, 0, stream, args);             \
         else if (small)                                                                        \
             hipLaunchKernelGGL(HIP_KERNEL_NAME(gemm_ring_kernel<E, 1>), grid, block, 0, stream, args);        \
